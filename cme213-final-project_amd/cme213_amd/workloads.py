@@ -1,0 +1,199 @@
+"""BASELINE workloads on the GPU: seeded synthetic inputs in HBM, the
+per-step call sequence through the C ABI, and the algorithmic byte counts
+the throughput figures use.
+
+Algorithmic bytes: every tensor a call reads is counted once and every
+tensor it writes once (fp32 = 4 B, ids = 4 B); a tensor updated in place
+(`+=` on a full activation, e.g. grad_residual) counts twice.  The two-pass
+partial rows of the column reductions are implementation overhead and are
+not counted.  Parameter-sized terms are included and negligible.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import (bias_gelu_forward, embedding_backward, embedding_pos_forward,
+               gelu_backward_with_bias_backward, layernorm_backward, layernorm_backward_residual,
+               layernorm_forward_save, pos_embedding_backward, residual_layernorm_forward_save)
+
+F32 = 4
+
+
+def ln_fwd_bytes(R, C):
+    return F32 * (2 * R * C + 2 * R + 2 * C)
+
+
+def ln_bwd_bytes(R, C):
+    return F32 * (3 * R * C + 2 * R + 3 * C)
+
+
+def res_ln_fwd_bytes(R, C):
+    return F32 * (4 * R * C + 2 * R + 2 * C)
+
+
+def ln_bwd_residual_bytes(R, C):
+    return F32 * (4 * R * C + 2 * R + 3 * C)
+
+
+def gelu_fwd_bytes(R, F):
+    return F32 * (2 * R * F + F)
+
+
+def gelu_bwd_bytes(R, F):
+    return F32 * (3 * R * F + 2 * F)
+
+
+def headline_bytes(R=8192, C=768, F=3072):
+    return {"ln_fwd": ln_fwd_bytes(R, C), "ln_bwd": ln_bwd_bytes(R, C),
+            "gelu_fwd": gelu_fwd_bytes(R, F), "gelu_bwd": gelu_bwd_bytes(R, F)}
+
+
+def _randn(shape, gen, scale=1.0, shift=0.0):
+    t = torch.randn(shape, device="cuda", generator=gen, dtype=torch.float32)
+    if scale != 1.0:
+        t.mul_(scale)
+    if shift != 0.0:
+        t.add_(shift)
+    return t
+
+
+class Headline:
+    """LN fwd+bwd on [R, C] and bias+GELU fwd+bwd on [R, F] (BASELINE metric,
+    B=8, T=1024, C=768, F=4C), over `sets` independent buffer sets so that
+    consecutive steps never find their inputs in the 256 MB last-level cache."""
+
+    def __init__(self, R=8192, C=768, F=3072, sets=3, seed=20260):
+        self.R, self.C, self.F = R, C, F
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        self.gamma = _randn((C,), g, 0.02, 1.0)
+        self.beta = _randn((C,), g, 0.02)
+        self.bias = _randn((F,), g, 0.02)
+        self.dgamma = torch.zeros(C, device="cuda")
+        self.dbeta = torch.zeros(C, device="cuda")
+        self.dbias = torch.zeros(F, device="cuda")
+        self.sets = []
+        for _ in range(sets):
+            s = {
+                "x": _randn((R, C), g), "dy": _randn((R, C), g),
+                "h": _randn((R, F), g, 1.5), "dh": _randn((R, F), g),
+                "y": torch.empty(R, C, device="cuda"), "dx": torch.empty(R, C, device="cuda"),
+                "mean": torch.empty(R, device="cuda"), "rstd": torch.empty(R, device="cuda"),
+                "o": torch.empty(R, F, device="cuda"), "gin": torch.empty(R, F, device="cuda"),
+            }
+            self.sets.append(s)
+        self.bytes = headline_bytes(R, C, F)
+        self.step_bytes = sum(self.bytes.values())
+
+    def ops(self, k):
+        s = self.sets[k % len(self.sets)]
+        R, C, F = self.R, self.C, self.F
+        return [
+            ("ln_fwd", lambda: layernorm_forward_save(s["x"], self.gamma, self.beta, s["y"],
+                                                      s["mean"], s["rstd"], R, C, 1e-5)),
+            ("ln_bwd", lambda: layernorm_backward(s["dy"], s["x"], s["mean"], s["rstd"],
+                                                  self.gamma, s["dx"], self.dgamma, self.dbeta,
+                                                  R, C)),
+            ("gelu_fwd", lambda: bias_gelu_forward(s["h"], self.bias, s["o"], R, F)),
+            ("gelu_bwd", lambda: gelu_backward_with_bias_backward(s["h"], self.bias, s["dh"],
+                                                                   s["gin"], self.dbias, R, F)),
+        ]
+
+    def step(self, k):
+        for _, fn in self.ops(k):
+            fn()
+
+    def host_inputs(self, k=0):
+        s = self.sets[k % len(self.sets)]
+        return {n: t.cpu().numpy() for n, t in
+                [("x", s["x"]), ("dy", s["dy"]), ("h", s["h"]), ("dh", s["dh"]),
+                 ("gamma", self.gamma), ("beta", self.beta), ("bias", self.bias)]}
+
+
+class BlockSequence:
+    """One GPT-2 block's non-GEMM sequence repeated over `layers` layers
+    (BASELINE configs 3 and 4).  Per layer, forward: r1 = r + a (fused with
+    LN1), r2 = r1 + m (fused with LN2), bias+GELU on [R, F]; backward in
+    reverse: GELU bwd + dbias, LN2 bwd accumulated into the residual-stream
+    gradient, LN1 bwd likewise.  a, m, the GELU pre-activation and the
+    upstream gradients stand in for the GEMM outputs (synthetic N(0,1))."""
+
+    def __init__(self, R, C, F, layers, seed=20263, shared_inputs=False):
+        self.R, self.C, self.F, self.L = R, C, F, layers
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        n_in = 1 if shared_inputs else layers
+        self.inp = [{"a": _randn((R, C), g), "m": _randn((R, C), g), "h": _randn((R, F), g),
+                     "gy1": _randn((R, C), g), "gy2": _randn((R, C), g), "gh": _randn((R, F), g)}
+                    for _ in range(n_in)]
+        self.params = [{"g1": _randn((C,), g, 0.02, 1.0), "b1": _randn((C,), g, 0.02),
+                        "g2": _randn((C,), g, 0.02, 1.0), "b2": _randn((C,), g, 0.02),
+                        "bias": _randn((F,), g, 0.02)} for _ in range(layers)]
+        self.grads = [{k: torch.zeros_like(v) for k, v in p.items()} for p in self.params]
+        self.r0 = _randn((R, C), g)
+        self.act = [{"r1": torch.empty(R, C, device="cuda"), "r2": torch.empty(R, C, device="cuda"),
+                     "y1": torch.empty(R, C, device="cuda"), "y2": torch.empty(R, C, device="cuda"),
+                     "m1": torch.empty(R, device="cuda"), "s1": torch.empty(R, device="cuda"),
+                     "m2": torch.empty(R, device="cuda"), "s2": torch.empty(R, device="cuda"),
+                     "o": torch.empty(R, F, device="cuda"), "gin": torch.empty(R, F, device="cuda")}
+                    for _ in range(layers)]
+        self.gres = torch.empty(R, C, device="cuda")
+        self.step_bytes = layers * (2 * res_ln_fwd_bytes(R, C) + gelu_fwd_bytes(R, F)
+                                    + gelu_bwd_bytes(R, F) + 2 * ln_bwd_residual_bytes(R, C))
+
+    def _in(self, l):
+        return self.inp[l % len(self.inp)]
+
+    def forward(self):
+        R, C, F = self.R, self.C, self.F
+        r = self.r0
+        for l in range(self.L):
+            i, p, a = self._in(l), self.params[l], self.act[l]
+            residual_layernorm_forward_save(r, i["a"], p["g1"], p["b1"], a["r1"], a["y1"], a["m1"],
+                                            a["s1"], R, C, 1e-5)
+            residual_layernorm_forward_save(a["r1"], i["m"], p["g2"], p["b2"], a["r2"], a["y2"],
+                                            a["m2"], a["s2"], R, C, 1e-5)
+            bias_gelu_forward(i["h"], p["bias"], a["o"], R, F)
+            r = a["r2"]
+        return r
+
+    def backward(self, gres_init):
+        R, C, F = self.R, self.C, self.F
+        self.gres.copy_(gres_init)
+        for l in reversed(range(self.L)):
+            i, p, a, gr = self._in(l), self.params[l], self.act[l], self.grads[l]
+            gelu_backward_with_bias_backward(i["h"], p["bias"], i["gh"], a["gin"], gr["bias"], R, F)
+            # LN2 normalised r2 = r1 + m and LN1 normalised r1 = r + a; the
+            # residual adds pass the stream gradient through unchanged.
+            layernorm_backward_residual(i["gy2"], a["r2"], a["m2"], a["s2"], p["g2"], self.gres,
+                                        gr["g2"], gr["b2"], R, C)
+            layernorm_backward_residual(i["gy1"], a["r1"], a["m1"], a["s1"], p["g1"], self.gres,
+                                        gr["g1"], gr["b1"], R, C)
+        return self.gres
+
+
+class Embedding:
+    """ids U[0, V) for B x T, wte [V, D], wpe [T, D]."""
+
+    def __init__(self, V=50257, D=768, B=16, T=1024, seed=20262):
+        self.V, self.D, self.B, self.T = V, D, B, T
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        self.wte = _randn((V, D), g, 0.02)
+        self.wpe = _randn((T, D), g, 0.02)
+        self.ids = torch.randint(0, V, (B * T,), device="cuda", generator=g, dtype=torch.int32)
+        self.dout = _randn((B * T, D), g)
+        self.out = torch.empty(B * T, D, device="cuda")
+        self.dwte = torch.zeros(V, D, device="cuda")
+        self.dwpe = torch.zeros(T, D, device="cuda")
+        self.distinct = int(torch.unique(self.ids).numel())
+        BT = B * T
+        self.fwd_bytes = F32 * (BT + 2 * BT * D + T * D)
+        self.bwd_bytes = F32 * (BT * D + BT + 2 * self.distinct * D + 2 * T * D)
+
+    def forward(self):
+        embedding_pos_forward(self.wte, self.wpe, self.ids, self.out, self.B, self.T, self.D, self.V)
+
+    def backward(self):
+        embedding_backward(self.dout, self.ids, self.dwte, self.B * self.T, self.D, self.V)
+        pos_embedding_backward(self.dout, self.dwpe, self.B, self.T, self.D)

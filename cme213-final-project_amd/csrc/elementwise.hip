@@ -1,0 +1,484 @@
+// Residual adds, bias broadcast, ReLU and tanh-GELU (forward and backward
+// with the bias gradient) for gfx950.
+//
+// Reference behaviour: FINAL_CLEAN_CODE/src/kernels/activations.cu:5-283
+// (residual_add, residual_add_with_bias, bias_add, bias_relu_forward,
+// relu_forward / relu_backward, relu_backward_with_bias_backward,
+// bias_backward).  GELU has no reference; it takes the bias+ReLU slots.
+//
+// Layout.  Bias-broadcast operators use a row-tiled grid: blockIdx.y picks
+// 256 consecutive W-wide column vectors, blockIdx.x a tile of rows; each
+// thread loads its bias vector once and walks the tile's rows, so there is
+// no per-element index division and every row access is a coalesced
+// 4 KiB stripe per workgroup.  Rows are processed in batches of kUnroll with
+// all loads of a batch issued before any arithmetic, to keep several
+// dwordx4 loads in flight per lane.
+//
+// Column reductions (dbias) are deterministic: each thread sums its column
+// over the tile's rows in row order and writes one partial row per tile;
+// colsum_finalize adds the tiles in a fixed order.  The reference uses
+// float atomicAdd here (activations.cu:231,271).
+#include "mi_common.hpp"
+
+#ifndef MI_REDUCE_TILES
+#define MI_REDUCE_TILES 256
+#endif
+
+namespace mi {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;
+
+// ---------------------------------------------------------------------------
+// tanh-approximation GELU (Hendrycks & Gimpel 2016):
+//   gelu(u) = 0.5 u (1 + tanh z),  z = sqrt(2/pi) (u + 0.044715 u^3).
+// With s = 0.5 (1 + tanh z) = 1 / (1 + e^{-2z}) (logistic of 2z):
+//   gelu(u)  = u s
+//   gelu'(u) = s + 2 u s (1 - s) z',  z' = sqrt(2/pi) (1 + 3*0.044715 u^2)
+//            = s (1 + 2 u (e s) z'),  since 1 - s = e s with e = e^{-2z}.
+// Neither form has the cancellation of 1 + tanh z for very negative u.
+// e^{-2z} is one v_exp_f32 (2^x) on -2 z log2(e), clamped to 2^126 so that
+// s and e*s stay finite (s then underflows towards 0, the correct limit);
+// 1 / (1 + e) is one v_rcp_f32.
+// ---------------------------------------------------------------------------
+constexpr float kGeluK0 = 0.7978845608028654f;   // sqrt(2/pi)
+constexpr float kGeluK1 = 0.044715f;
+constexpr float kM2Log2e = -2.8853900817779268f;  // -2 * log2(e)
+
+struct GeluTerms {
+    float s;  // 1 / (1 + e^{-2z})
+    float e;  // e^{-2z}
+};
+
+__device__ __forceinline__ GeluTerms gelu_terms(float u) {
+    const float u2 = u * u;
+    const float z = kGeluK0 * fmaf(kGeluK1 * u2, u, u);
+    const float t = fminf(kM2Log2e * z, 126.0f);
+    const float e = __builtin_amdgcn_exp2f(t);
+    return {__builtin_amdgcn_rcpf(1.0f + e), e};
+}
+
+__device__ __forceinline__ float gelu_fwd(float u) { return u * gelu_terms(u).s; }
+
+__device__ __forceinline__ float gelu_grad(float u) {
+    const GeluTerms g = gelu_terms(u);
+    const float dz = kGeluK0 * fmaf(3.0f * kGeluK1, u * u, 1.0f);
+    return g.s * fmaf(2.0f * u * (g.e * g.s), dz, 1.0f);
+}
+
+// ---------------------------------------------------------------------------
+// Flat element-wise kernels (no broadcast).  Pointers may alias (the
+// reference allows residual_add(a, b, a)); each element is read and written
+// by one thread, so aliasing is safe without __restrict__.
+// ---------------------------------------------------------------------------
+template <int W>
+struct AddOp {
+    const float* a;
+    const float* b;
+    float* out;
+    __device__ void operator()(size_t i) const {
+        const fvec<W> x = vload<W>(a, i), y = vload<W>(b, i);
+        fvec<W> o;
+#pragma unroll
+        for (int e = 0; e < W; ++e) o.v[e] = x.v[e] + y.v[e];
+        vstore<W>(out, i, o);
+    }
+};
+
+template <int W>
+struct ReluOp {
+    const float* in;
+    float* out;
+    __device__ void operator()(size_t i) const {
+        const fvec<W> x = vload<W>(in, i);
+        fvec<W> o;
+#pragma unroll
+        for (int e = 0; e < W; ++e) o.v[e] = (x.v[e] > 0.0f) ? x.v[e] : 0.0f;
+        vstore<W>(out, i, o);
+    }
+};
+
+template <int W>
+struct ReluBwdOp {
+    const float* in;
+    const float* g;
+    float* gin;
+    __device__ void operator()(size_t i) const {
+        const fvec<W> x = vload<W>(in, i), d = vload<W>(g, i);
+        fvec<W> o;
+#pragma unroll
+        for (int e = 0; e < W; ++e) o.v[e] = (x.v[e] > 0.0f) ? d.v[e] : 0.0f;
+        vstore<W>(gin, i, o);
+    }
+};
+
+template <class Op>
+__global__ __launch_bounds__(kThreads) void flat_kernel(Op op, long long nvec) {
+    const long long stride = static_cast<long long>(gridDim.x) * kThreads;
+    for (long long i = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x; i < nvec;
+         i += stride)
+        op(static_cast<size_t>(i));
+}
+
+template <class Op>
+int launch_flat(const char* name, Op op, long long nvec, hipStream_t st) {
+    if (nvec <= 0) return MI_OK;
+    long long grid = (nvec + kThreads - 1) / kThreads;
+    if (grid > 16384) grid = 16384;
+    hipLaunchKernelGGL(flat_kernel<Op>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, st,
+                       op, nvec);
+    return check_launch(name);
+}
+
+// ---------------------------------------------------------------------------
+// Row-tiled broadcast kernels.  An Op provides
+//   In load(size_t vec_index) const;          // HBM loads of one vector
+//   fvec<W> apply(size_t vec_index, const In&, const fvec<W>& bias) const;
+// apply() writes the output vector (if any) and returns the vector that
+// contributes to the column sum (ignored by the non-reducing kernel).
+// ---------------------------------------------------------------------------
+template <int W, class Op, bool REDUCE>
+__global__ __launch_bounds__(kThreads) void rowtile_kernel(Op op, const float* __restrict__ bias,
+                                                           float* __restrict__ part, int rows,
+                                                           int nv, int rpt) {
+    const int j = blockIdx.y * kThreads + threadIdx.x;
+    if (j >= nv) return;
+    const int r0 = blockIdx.x * rpt;
+    const int r1 = min(r0 + rpt, rows);
+    const fvec<W> bv = bias ? vload<W>(bias, j) : vzero<W>();
+    fvec<W> acc = vzero<W>();
+    int r = r0;
+    for (; r + kUnroll <= r1; r += kUnroll) {
+        typename Op::In in[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u)
+            in[u] = op.load(static_cast<size_t>(r + u) * nv + j);
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const fvec<W> c = op.apply(static_cast<size_t>(r + u) * nv + j, in[u], bv);
+            if constexpr (REDUCE) {
+#pragma unroll
+                for (int e = 0; e < W; ++e) acc.v[e] += c.v[e];
+            }
+        }
+    }
+    for (; r < r1; ++r) {
+        const typename Op::In in = op.load(static_cast<size_t>(r) * nv + j);
+        const fvec<W> c = op.apply(static_cast<size_t>(r) * nv + j, in, bv);
+        if constexpr (REDUCE) {
+#pragma unroll
+            for (int e = 0; e < W; ++e) acc.v[e] += c.v[e];
+        }
+    }
+    if constexpr (REDUCE) vstore<W>(part + static_cast<size_t>(blockIdx.x) * nv * W, j, acc);
+}
+
+template <int W>
+struct ResidBiasOp {  // out = (a + x) + bias
+    const float* a;
+    const float* x;
+    float* out;
+    struct In {
+        fvec<W> a, x;
+    };
+    __device__ In load(size_t i) const { return {vload<W>(a, i), vload<W>(x, i)}; }
+    __device__ fvec<W> apply(size_t i, const In& in, const fvec<W>& b) const {
+        fvec<W> o;
+#pragma unroll
+        for (int e = 0; e < W; ++e) o.v[e] = in.a.v[e] + in.x.v[e] + b.v[e];
+        vstore<W>(out, i, o);
+        return o;
+    }
+};
+
+template <int W>
+struct BiasAddOp {  // out += bias (in place)
+    float* out;
+    struct In {
+        fvec<W> o;
+    };
+    __device__ In load(size_t i) const { return {vload<W>(out, i)}; }
+    __device__ fvec<W> apply(size_t i, const In& in, const fvec<W>& b) const {
+        fvec<W> o;
+#pragma unroll
+        for (int e = 0; e < W; ++e) o.v[e] = in.o.v[e] + b.v[e];
+        vstore<W>(out, i, o);
+        return o;
+    }
+};
+
+template <int W>
+struct BiasReluOp {  // out = max(in + bias, 0)
+    const float* in;
+    float* out;
+    struct In {
+        fvec<W> x;
+    };
+    __device__ In load(size_t i) const { return {vload<W>(in, i)}; }
+    __device__ fvec<W> apply(size_t i, const In& v, const fvec<W>& b) const {
+        fvec<W> o;
+#pragma unroll
+        for (int e = 0; e < W; ++e) {
+            const float t = v.x.v[e] + b.v[e];
+            o.v[e] = (t > 0.0f) ? t : 0.0f;
+        }
+        vstore<W>(out, i, o);
+        return o;
+    }
+};
+
+template <int W>
+struct BiasGeluOp {  // out = gelu(in + bias)
+    const float* in;
+    float* out;
+    struct In {
+        fvec<W> x;
+    };
+    __device__ In load(size_t i) const { return {vload<W>(in, i)}; }
+    __device__ fvec<W> apply(size_t i, const In& v, const fvec<W>& b) const {
+        fvec<W> o;
+#pragma unroll
+        for (int e = 0; e < W; ++e) o.v[e] = gelu_fwd(v.x.v[e] + b.v[e]);
+        vstore<W>(out, i, o);
+        return o;
+    }
+};
+
+template <int W>
+struct ColSumOp {  // dbias partials of grad
+    const float* g;
+    struct In {
+        fvec<W> g;
+    };
+    __device__ In load(size_t i) const { return {vload<W>(g, i)}; }
+    __device__ fvec<W> apply(size_t, const In& v, const fvec<W>&) const { return v.g; }
+};
+
+template <int W>
+struct ReluBwdBiasOp {  // gin = mask > 0 ? g : 0
+    const float* mask;
+    const float* g;
+    float* gin;
+    struct In {
+        fvec<W> m, g;
+    };
+    __device__ In load(size_t i) const { return {vload<W>(mask, i), vload<W>(g, i)}; }
+    __device__ fvec<W> apply(size_t i, const In& v, const fvec<W>&) const {
+        fvec<W> o;
+#pragma unroll
+        for (int e = 0; e < W; ++e) o.v[e] = (v.m.v[e] > 0.0f) ? v.g.v[e] : 0.0f;
+        vstore<W>(gin, i, o);
+        return o;
+    }
+};
+
+template <int W>
+struct GeluBwdBiasOp {  // gin = g * gelu'(in + bias)
+    const float* in;
+    const float* g;
+    float* gin;
+    struct In {
+        fvec<W> x, g;
+    };
+    __device__ In load(size_t i) const { return {vload<W>(in, i), vload<W>(g, i)}; }
+    __device__ fvec<W> apply(size_t i, const In& v, const fvec<W>& b) const {
+        fvec<W> o;
+#pragma unroll
+        for (int e = 0; e < W; ++e) o.v[e] = v.g.v[e] * gelu_grad(v.x.v[e] + b.v[e]);
+        vstore<W>(gin, i, o);
+        return o;
+    }
+};
+
+int check_shape(const char* name, int rows, int cols) {
+    if (rows < 0 || cols <= 0)
+        return set_error(MI_ERR_INVALID_ARG, "%s: invalid shape rows=%d cols=%d", name, rows,
+                         cols);
+    return MI_OK;
+}
+
+// Rows per tile for the non-reducing broadcast kernels.
+constexpr int kFwdRowsPerTile = 8;
+
+template <int W, class Op>
+int launch_rowtile(const char* name, Op op, const float* bias, int rows, int cols,
+                   hipStream_t st) {
+    const int nv = cols / W;
+    const int rpt = kFwdRowsPerTile;
+    const dim3 grid((rows + rpt - 1) / rpt, (nv + kThreads - 1) / kThreads);
+    hipLaunchKernelGGL((rowtile_kernel<W, Op, false>), grid, dim3(kThreads), 0, st, op, bias,
+                       nullptr, rows, nv, rpt);
+    return check_launch(name);
+}
+
+// Tiles for the reducing kernels: about MI_REDUCE_TILES partial rows, at
+// least 4 rows per tile.  Depends only on the shape, so the summation order
+// is fixed for a given shape.
+struct ReducePlan {
+    int rpt;
+    int tiles;
+};
+
+ReducePlan plan_reduce(int rows) {
+    int rpt = (rows + MI_REDUCE_TILES - 1) / MI_REDUCE_TILES;
+    if (rpt < 4) rpt = 4;
+    return {rpt, (rows + rpt - 1) / rpt};
+}
+
+template <int W, class Op>
+int launch_rowtile_reduce(const char* name, Op op, const float* bias, float* dbias, int rows,
+                          int cols, hipStream_t st) {
+    const ReducePlan p = plan_reduce(rows);
+    int err = MI_OK;
+    float* part = static_cast<float*>(
+        workspace_get(static_cast<size_t>(p.tiles) * cols * sizeof(float), st, &err));
+    if (!part) return err;
+    const int nv = cols / W;
+    const dim3 grid(p.tiles, (nv + kThreads - 1) / kThreads);
+    hipLaunchKernelGGL((rowtile_kernel<W, Op, true>), grid, dim3(kThreads), 0, st, op, bias, part,
+                       rows, nv, p.rpt);
+    int rc = check_launch(name);
+    if (rc != MI_OK) return rc;
+    return launch_colsum_finalize(part, p.tiles, cols, dbias, cols, nullptr, st);
+}
+
+bool all_aligned(std::initializer_list<const void*> ps) {
+    for (const void* p : ps)
+        if (p && !aligned16(p)) return false;
+    return true;
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" {
+
+size_t mi_bias_backward_workspace(int rows, int cols) {
+    if (rows <= 0 || cols <= 0) return 0;
+    return static_cast<size_t>(plan_reduce(rows).tiles) * cols * sizeof(float);
+}
+
+int mi_residual_add(const float* a, const float* b, float* out, long long n, void* stream) {
+    if (n < 0) return set_error(MI_ERR_INVALID_ARG, "mi_residual_add: n=%lld", n);
+    if (n == 0) return MI_OK;
+    if (!a || !b || !out) return set_error(MI_ERR_INVALID_ARG, "mi_residual_add: NULL pointer");
+    if (n % 4 == 0 && all_aligned({a, b, out}))
+        return launch_flat("mi_residual_add", AddOp<4>{a, b, out}, n / 4, to_stream(stream));
+    return launch_flat("mi_residual_add", AddOp<1>{a, b, out}, n, to_stream(stream));
+}
+
+int mi_relu_forward(const float* in, float* out, long long n, void* stream) {
+    if (n < 0) return set_error(MI_ERR_INVALID_ARG, "mi_relu_forward: n=%lld", n);
+    if (n == 0) return MI_OK;
+    if (!in || !out) return set_error(MI_ERR_INVALID_ARG, "mi_relu_forward: NULL pointer");
+    if (n % 4 == 0 && all_aligned({in, out}))
+        return launch_flat("mi_relu_forward", ReluOp<4>{in, out}, n / 4, to_stream(stream));
+    return launch_flat("mi_relu_forward", ReluOp<1>{in, out}, n, to_stream(stream));
+}
+
+int mi_relu_backward(const float* in, const float* grad_out, float* grad_in, long long n,
+                     void* stream) {
+    if (n < 0) return set_error(MI_ERR_INVALID_ARG, "mi_relu_backward: n=%lld", n);
+    if (n == 0) return MI_OK;
+    if (!in || !grad_out || !grad_in)
+        return set_error(MI_ERR_INVALID_ARG, "mi_relu_backward: NULL pointer");
+    if (n % 4 == 0 && all_aligned({in, grad_out, grad_in}))
+        return launch_flat("mi_relu_backward", ReluBwdOp<4>{in, grad_out, grad_in}, n / 4,
+                           to_stream(stream));
+    return launch_flat("mi_relu_backward", ReluBwdOp<1>{in, grad_out, grad_in}, n,
+                       to_stream(stream));
+}
+
+int mi_residual_add_with_bias(const float* residual, const float* x, const float* bias,
+                              float* out, int rows, int cols, void* stream) {
+    const char* name = "mi_residual_add_with_bias";
+    if (int rc = check_shape(name, rows, cols)) return rc;
+    if (rows == 0) return MI_OK;
+    if (!residual || !x || !bias || !out) return set_error(MI_ERR_INVALID_ARG, "%s: NULL", name);
+    if (cols % 4 == 0 && all_aligned({residual, x, bias, out}))
+        return launch_rowtile<4>(name, ResidBiasOp<4>{residual, x, out}, bias, rows, cols,
+                                 to_stream(stream));
+    return launch_rowtile<1>(name, ResidBiasOp<1>{residual, x, out}, bias, rows, cols,
+                             to_stream(stream));
+}
+
+int mi_bias_add(float* out, const float* bias, int rows, int cols, void* stream) {
+    const char* name = "mi_bias_add";
+    if (int rc = check_shape(name, rows, cols)) return rc;
+    if (rows == 0) return MI_OK;
+    if (!bias || !out) return set_error(MI_ERR_INVALID_ARG, "%s: NULL", name);
+    if (cols % 4 == 0 && all_aligned({bias, out}))
+        return launch_rowtile<4>(name, BiasAddOp<4>{out}, bias, rows, cols, to_stream(stream));
+    return launch_rowtile<1>(name, BiasAddOp<1>{out}, bias, rows, cols, to_stream(stream));
+}
+
+int mi_bias_relu_forward(const float* in, const float* bias, float* out, int rows, int cols,
+                         void* stream) {
+    const char* name = "mi_bias_relu_forward";
+    if (int rc = check_shape(name, rows, cols)) return rc;
+    if (rows == 0) return MI_OK;
+    if (!in || !bias || !out) return set_error(MI_ERR_INVALID_ARG, "%s: NULL", name);
+    if (cols % 4 == 0 && all_aligned({in, bias, out}))
+        return launch_rowtile<4>(name, BiasReluOp<4>{in, out}, bias, rows, cols,
+                                 to_stream(stream));
+    return launch_rowtile<1>(name, BiasReluOp<1>{in, out}, bias, rows, cols, to_stream(stream));
+}
+
+int mi_bias_gelu_forward(const float* in, const float* bias, float* out, int rows, int cols,
+                         void* stream) {
+    const char* name = "mi_bias_gelu_forward";
+    if (int rc = check_shape(name, rows, cols)) return rc;
+    if (rows == 0) return MI_OK;
+    if (!in || !bias || !out) return set_error(MI_ERR_INVALID_ARG, "%s: NULL", name);
+    if (cols % 4 == 0 && all_aligned({in, bias, out}))
+        return launch_rowtile<4>(name, BiasGeluOp<4>{in, out}, bias, rows, cols,
+                                 to_stream(stream));
+    return launch_rowtile<1>(name, BiasGeluOp<1>{in, out}, bias, rows, cols, to_stream(stream));
+}
+
+int mi_bias_backward(const float* grad, float* dbias, int rows, int cols, void* stream) {
+    const char* name = "mi_bias_backward";
+    if (int rc = check_shape(name, rows, cols)) return rc;
+    if (rows == 0) return MI_OK;
+    if (!grad || !dbias) return set_error(MI_ERR_INVALID_ARG, "%s: NULL", name);
+    if (cols % 4 == 0 && all_aligned({grad}))
+        return launch_rowtile_reduce<4>(name, ColSumOp<4>{grad}, nullptr, dbias, rows, cols,
+                                        to_stream(stream));
+    return launch_rowtile_reduce<1>(name, ColSumOp<1>{grad}, nullptr, dbias, rows, cols,
+                                    to_stream(stream));
+}
+
+int mi_relu_backward_with_bias_backward(const float* mask, const float* grad_out, float* grad_in,
+                                        float* dbias, int rows, int cols, void* stream) {
+    const char* name = "mi_relu_backward_with_bias_backward";
+    if (int rc = check_shape(name, rows, cols)) return rc;
+    if (rows == 0) return MI_OK;
+    if (!mask || !grad_out || !grad_in || !dbias)
+        return set_error(MI_ERR_INVALID_ARG, "%s: NULL", name);
+    if (cols % 4 == 0 && all_aligned({mask, grad_out, grad_in}))
+        return launch_rowtile_reduce<4>(name, ReluBwdBiasOp<4>{mask, grad_out, grad_in}, nullptr,
+                                        dbias, rows, cols, to_stream(stream));
+    return launch_rowtile_reduce<1>(name, ReluBwdBiasOp<1>{mask, grad_out, grad_in}, nullptr,
+                                    dbias, rows, cols, to_stream(stream));
+}
+
+int mi_gelu_backward_with_bias_backward(const float* in, const float* bias,
+                                        const float* grad_out, float* grad_in, float* dbias,
+                                        int rows, int cols, void* stream) {
+    const char* name = "mi_gelu_backward_with_bias_backward";
+    if (int rc = check_shape(name, rows, cols)) return rc;
+    if (rows == 0) return MI_OK;
+    if (!in || !bias || !grad_out || !grad_in || !dbias)
+        return set_error(MI_ERR_INVALID_ARG, "%s: NULL", name);
+    if (cols % 4 == 0 && all_aligned({in, bias, grad_out, grad_in}))
+        return launch_rowtile_reduce<4>(name, GeluBwdBiasOp<4>{in, grad_out, grad_in}, bias,
+                                        dbias, rows, cols, to_stream(stream));
+    return launch_rowtile_reduce<1>(name, GeluBwdBiasOp<1>{in, grad_out, grad_in}, bias, dbias,
+                                    rows, cols, to_stream(stream));
+}
+
+}  // extern "C"

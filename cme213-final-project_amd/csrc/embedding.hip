@@ -1,0 +1,428 @@
+// Token + position embedding for gfx950.
+//
+// Reference behaviour: FINAL_CLEAN_CODE/src/kernels/embedding.cu (gather,
+// in-place position add, float-atomic scatter-add backward) and the CPU
+// loops of NEW_code/tests/test_embedding.cu:16-41.
+//
+// Forward: one wave per token row, W-wide vector copies; the fused variant
+// writes table[id] + pos[t] in one pass (one fp32 add, so bit-identical to
+// the reference's gather followed by its in-place add).
+//
+// Token backward, deterministic and bit-identical to the CPU loop, which
+// adds grad rows into grad_table in increasing token position:
+//   1. keys = ids (invalid ids -> a sentinel that sorts last), vals = i;
+//   2. stable LSD radix sort of (key, val), 8-bit digits, only as many
+//      passes as the key range needs.  Each pass: per-tile digit histogram
+//      (LDS integer counters), one exclusive scan over (digit, tile), and a
+//      stable scatter where one wave ranks its tile's elements 64 at a time
+//      in index order (ballot-based digit match + popcount);
+//   3. one wave per run of equal keys: load grad_table[key] once, add the
+//      run's grad rows in sorted (= increasing i) order, store once.
+// Position backward: one thread per (t, column vector) adds grad_out[b, t]
+// for b = 0, 1, ... in order onto grad_pos[t].
+#include "mi_common.hpp"
+
+namespace mi {
+
+namespace {
+
+constexpr int kRowWaves = 4;   // token rows per workgroup
+constexpr int kTile = 1024;    // radix tile: 16 batches of 64
+constexpr int kDigits = 256;
+constexpr unsigned kSentinel = 0xFFFFFFFFu;
+
+// ---------------------------------------------------------------------------
+// Forward
+// ---------------------------------------------------------------------------
+template <int W, bool POS>
+__global__ __launch_bounds__(kRowWaves * kWave) void emb_fwd_kernel(
+    const float* __restrict__ table, const float* __restrict__ pos, const int* __restrict__ tokens,
+    float* __restrict__ out, int batch_seq, int seq, int dim, int vocab) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int i = blockIdx.x * kRowWaves + static_cast<int>(threadIdx.x / kWave);
+    if (i >= batch_seq) return;
+    const int id = tokens[i];
+    const bool ok = vocab <= 0 || (id >= 0 && id < vocab);
+    const int nv = dim / W;
+    const float* src = table + static_cast<size_t>(ok ? id : 0) * dim;
+    const float* p = POS ? pos + static_cast<size_t>(i % seq) * dim : nullptr;
+    float* dst = out + static_cast<size_t>(i) * dim;
+#pragma unroll 4
+    for (int j = lane; j < nv; j += kWave) {
+        fvec<W> v = ok ? vload<W>(src, j) : vzero<W>();
+        if constexpr (POS) {
+            const fvec<W> q = vload<W>(p, j);
+#pragma unroll
+            for (int e = 0; e < W; ++e) v.v[e] = v.v[e] + q.v[e];
+        }
+        vstore<W>(dst, j, v);
+    }
+}
+
+// embeddings[b, t, :] += pos[t, :], one wave per row.
+template <int W>
+__global__ __launch_bounds__(kRowWaves * kWave) void pos_add_kernel(const float* __restrict__ pos,
+                                                                    float* __restrict__ emb,
+                                                                    int rows, int seq, int dim) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int i = blockIdx.x * kRowWaves + static_cast<int>(threadIdx.x / kWave);
+    if (i >= rows) return;
+    const int nv = dim / W;
+    const float* p = pos + static_cast<size_t>(i % seq) * dim;
+    float* dst = emb + static_cast<size_t>(i) * dim;
+#pragma unroll 4
+    for (int j = lane; j < nv; j += kWave) {
+        fvec<W> v = vload<W>(dst, j);
+        const fvec<W> q = vload<W>(p, j);
+#pragma unroll
+        for (int e = 0; e < W; ++e) v.v[e] = v.v[e] + q.v[e];
+        vstore<W>(dst, j, v);
+    }
+}
+
+// grad_pos[t, j] += grad_out[b, t, j] for b = 0..batch-1 in order.
+template <int W>
+__global__ __launch_bounds__(256) void pos_bwd_kernel(const float* __restrict__ g,
+                                                      float* __restrict__ gpos, int batch,
+                                                      int seq, int dim) {
+    const int nv = dim / W;
+    const long long idx = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= static_cast<long long>(seq) * nv) return;
+    const int t = static_cast<int>(idx / nv);
+    const int j = static_cast<int>(idx % nv);
+    const size_t row_stride = static_cast<size_t>(seq) * nv;  // in vectors
+    const size_t base = static_cast<size_t>(t) * nv + j;
+    fvec<W> acc = vload<W>(gpos, base);
+    int b = 0;
+    for (; b + 4 <= batch; b += 4) {
+        fvec<W> q[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) q[u] = vload<W>(g, base + (b + u) * row_stride);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int e = 0; e < W; ++e) acc.v[e] = acc.v[e] + q[u].v[e];
+    }
+    for (; b < batch; ++b) {
+        const fvec<W> q = vload<W>(g, base + b * row_stride);
+#pragma unroll
+        for (int e = 0; e < W; ++e) acc.v[e] = acc.v[e] + q.v[e];
+    }
+    vstore<W>(gpos, base, acc);
+}
+
+// ---------------------------------------------------------------------------
+// Stable LSD radix sort of (key, val) pairs.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void prep_keys_kernel(const int* __restrict__ ids,
+                                                        unsigned* __restrict__ keys,
+                                                        int* __restrict__ vals, int n, int vocab) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const int id = ids[i];
+    const bool ok = id >= 0 && (vocab <= 0 || id < vocab);
+    keys[i] = ok ? static_cast<unsigned>(id) : kSentinel;
+    vals[i] = i;
+}
+
+// hist[d * ntiles + tile] = number of keys of the tile whose digit is d.
+__global__ __launch_bounds__(256) void radix_hist_kernel(const unsigned* __restrict__ keys, int n,
+                                                         int shift, int ntiles,
+                                                         int* __restrict__ hist) {
+    __shared__ int cnt[kDigits];
+    cnt[threadIdx.x] = 0;
+    __syncthreads();
+    const int base = blockIdx.x * kTile;
+    for (int k = threadIdx.x; k < kTile; k += 256) {
+        const int e = base + k;
+        if (e < n) atomicAdd(&cnt[(keys[e] >> shift) & (kDigits - 1)], 1);
+    }
+    __syncthreads();
+    hist[threadIdx.x * ntiles + blockIdx.x] = cnt[threadIdx.x];
+}
+
+// In-place exclusive scan of m ints by one 1024-thread workgroup.
+__global__ __launch_bounds__(1024) void exclusive_scan_kernel(int* __restrict__ data, int m) {
+    __shared__ int wsum[16];
+    __shared__ int carry_s;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    if (threadIdx.x == 0) carry_s = 0;
+    __syncthreads();
+    for (int base = 0; base < m; base += 1024) {
+        const int i = base + threadIdx.x;
+        const int v = i < m ? data[i] : 0;
+        // inclusive wave scan (Hillis-Steele over 64 lanes)
+        int x = v;
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {
+            const int y = __shfl_up(x, off, kWave);
+            if (lane >= off) x += y;
+        }
+        if (lane == kWave - 1) wsum[wave] = x;
+        __syncthreads();
+        int before = carry_s;
+        for (int w = 0; w < wave; ++w) before += wsum[w];
+        if (i < m) data[i] = before + x - v;
+        __syncthreads();
+        if (threadIdx.x == 1023) carry_s = before + x;
+        __syncthreads();
+    }
+}
+
+// Stable scatter of one tile by one wave; offs = scanned hist.
+__global__ __launch_bounds__(kWave) void radix_scatter_kernel(
+    const unsigned* __restrict__ kin, const int* __restrict__ vin, unsigned* __restrict__ kout,
+    int* __restrict__ vout, int n, int shift, int ntiles, const int* __restrict__ offs) {
+    __shared__ int run[kDigits];
+    const int lane = threadIdx.x;
+    const int tile = blockIdx.x;
+#pragma unroll
+    for (int d = lane; d < kDigits; d += kWave) run[d] = offs[d * ntiles + tile];
+    __syncthreads();
+    const unsigned long long below = (1ull << lane) - 1ull;
+    for (int b = 0; b < kTile / kWave; ++b) {
+        const int e = tile * kTile + b * kWave + lane;
+        const bool valid = e < n;
+        const unsigned key = valid ? kin[e] : 0u;
+        const int val = valid ? vin[e] : 0;
+        const int d = static_cast<int>((key >> shift) & (kDigits - 1));
+        unsigned long long peers = __ballot(valid);
+#pragma unroll
+        for (int bit = 0; bit < 8; ++bit) {
+            const bool set = (d >> bit) & 1;
+            const unsigned long long m = __ballot(set);
+            peers &= set ? m : ~m;
+        }
+        const int rank = __popcll(peers & below);
+        const int pos = run[d] + rank;
+        const bool leader = valid && (63 - __clzll(peers)) == lane;
+        __syncthreads();  // every lane has read run[] before the leaders update it
+        if (valid) {
+            kout[pos] = key;
+            vout[pos] = val;
+        }
+        if (leader) run[d] += __popcll(peers);
+        __syncthreads();
+    }
+}
+
+// One wave per sorted position; the first position of each run of equal
+// keys accumulates the run's grad rows, in sorted order, onto its table row.
+template <int W, int NCH>
+__global__ __launch_bounds__(kRowWaves * kWave) void emb_bwd_accum_kernel(
+    const unsigned* __restrict__ keys, const int* __restrict__ vals, int n,
+    const float* __restrict__ g, float* __restrict__ table, int dim) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int s = blockIdx.x * kRowWaves + static_cast<int>(threadIdx.x / kWave);
+    if (s >= n) return;
+    const unsigned key = keys[s];
+    if (key == kSentinel) return;
+    if (s > 0 && keys[s - 1] == key) return;
+    // Find the end of the run, 64 keys at a time.
+    int end = s + 1;
+    for (;;) {
+        const int e = end + lane;
+        const bool same = e < n && keys[e] == key;
+        const unsigned long long m = __ballot(same);
+        const unsigned long long miss = ~m;
+        const int first_miss =
+            miss ? __ffsll(static_cast<unsigned long long>(miss)) - 1 : kWave;  // 0..64
+        end += first_miss;
+        if (first_miss < kWave) break;
+    }
+    const int nv = dim / W;
+    float* trow = table + static_cast<size_t>(key) * dim;
+    for (int c0 = 0; c0 < nv; c0 += NCH * kWave) {
+        fvec<W> acc[NCH];
+#pragma unroll
+        for (int k = 0; k < NCH; ++k) {
+            const int j = c0 + lane + k * kWave;
+            acc[k] = j < nv ? vload<W>(trow, j) : vzero<W>();
+        }
+        for (int b0 = s; b0 < end; b0 += kWave) {
+            const int cnt = min(kWave, end - b0);
+            const int my_i = (b0 + lane < end) ? vals[b0 + lane] : 0;
+            for (int q = 0; q < cnt; ++q) {
+                const int i = __shfl(my_i, q, kWave);
+                const float* grow = g + static_cast<size_t>(i) * dim;
+#pragma unroll
+                for (int k = 0; k < NCH; ++k) {
+                    const int j = c0 + lane + k * kWave;
+                    if (j < nv) {
+                        const fvec<W> v = vload<W>(grow, j);
+#pragma unroll
+                        for (int e = 0; e < W; ++e) acc[k].v[e] = acc[k].v[e] + v.v[e];
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < NCH; ++k) {
+            const int j = c0 + lane + k * kWave;
+            if (j < nv) vstore<W>(trow, j, acc[k]);
+        }
+    }
+}
+
+struct SortPlan {
+    int ntiles;
+    int passes;
+    size_t bytes;
+    size_t off_k1, off_v0, off_v1, off_hist;
+};
+
+SortPlan plan_sort(int n, int vocab) {
+    SortPlan p;
+    p.ntiles = (n + kTile - 1) / kTile;
+    int bits = 32;
+    if (vocab > 0) {
+        // Keys are ids in [0, vocab) or the sentinel, whose low `bits` bits
+        // are all ones and so still sort after every id below 2^bits.
+        bits = 1;
+        while (bits < 32 && (1u << bits) <= static_cast<unsigned>(vocab)) ++bits;
+    }
+    p.passes = (bits + 7) / 8;
+    const size_t a = round_up(static_cast<size_t>(n) * 4, 256);
+    p.off_k1 = a;
+    p.off_v0 = 2 * a;
+    p.off_v1 = 3 * a;
+    p.off_hist = 4 * a;
+    p.bytes = p.off_hist + round_up(static_cast<size_t>(p.ntiles) * kDigits * 4, 256);
+    return p;
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" {
+
+size_t mi_embedding_backward_workspace(int batch_seq) {
+    if (batch_seq <= 0) return 0;
+    return plan_sort(batch_seq, 0).bytes;
+}
+
+int mi_embedding_forward(const float* table, const int* tokens, float* out, int batch_seq,
+                         int dim, int vocab, void* stream) {
+    const char* name = "mi_embedding_forward";
+    if (batch_seq < 0 || dim <= 0)
+        return set_error(MI_ERR_INVALID_ARG, "%s: batch_seq=%d dim=%d", name, batch_seq, dim);
+    if (batch_seq == 0) return MI_OK;
+    if (!table || !tokens || !out) return set_error(MI_ERR_INVALID_ARG, "%s: NULL", name);
+    const dim3 grid((batch_seq + kRowWaves - 1) / kRowWaves), block(kRowWaves * kWave);
+    hipStream_t st = to_stream(stream);
+    if (dim % 4 == 0 && aligned16(table) && aligned16(out))
+        hipLaunchKernelGGL((emb_fwd_kernel<4, false>), grid, block, 0, st, table, nullptr, tokens,
+                           out, batch_seq, 1, dim, vocab);
+    else
+        hipLaunchKernelGGL((emb_fwd_kernel<1, false>), grid, block, 0, st, table, nullptr, tokens,
+                           out, batch_seq, 1, dim, vocab);
+    return check_launch(name);
+}
+
+int mi_embedding_pos_forward(const float* table, const float* pos_table, const int* tokens,
+                             float* out, int batch, int seq, int dim, int vocab, void* stream) {
+    const char* name = "mi_embedding_pos_forward";
+    if (batch < 0 || seq <= 0 || dim <= 0)
+        return set_error(MI_ERR_INVALID_ARG, "%s: batch=%d seq=%d dim=%d", name, batch, seq, dim);
+    const long long bt = static_cast<long long>(batch) * seq;
+    if (bt == 0) return MI_OK;
+    if (bt > INT32_MAX) return set_error(MI_ERR_INVALID_ARG, "%s: batch*seq too large", name);
+    if (!table || !pos_table || !tokens || !out)
+        return set_error(MI_ERR_INVALID_ARG, "%s: NULL", name);
+    const dim3 grid(static_cast<unsigned>((bt + kRowWaves - 1) / kRowWaves)),
+        block(kRowWaves * kWave);
+    hipStream_t st = to_stream(stream);
+    if (dim % 4 == 0 && aligned16(table) && aligned16(pos_table) && aligned16(out))
+        hipLaunchKernelGGL((emb_fwd_kernel<4, true>), grid, block, 0, st, table, pos_table, tokens,
+                           out, static_cast<int>(bt), seq, dim, vocab);
+    else
+        hipLaunchKernelGGL((emb_fwd_kernel<1, true>), grid, block, 0, st, table, pos_table, tokens,
+                           out, static_cast<int>(bt), seq, dim, vocab);
+    return check_launch(name);
+}
+
+int mi_pos_embedding_forward(const float* pos_table, float* embeddings, int batch, int seq,
+                             int dim, void* stream) {
+    const char* name = "mi_pos_embedding_forward";
+    if (batch < 0 || seq <= 0 || dim <= 0)
+        return set_error(MI_ERR_INVALID_ARG, "%s: batch=%d seq=%d dim=%d", name, batch, seq, dim);
+    const long long rows = static_cast<long long>(batch) * seq;
+    if (rows == 0) return MI_OK;
+    if (rows > INT32_MAX) return set_error(MI_ERR_INVALID_ARG, "%s: batch*seq too large", name);
+    if (!pos_table || !embeddings) return set_error(MI_ERR_INVALID_ARG, "%s: NULL", name);
+    const dim3 grid(static_cast<unsigned>((rows + kRowWaves - 1) / kRowWaves)),
+        block(kRowWaves * kWave);
+    hipStream_t st = to_stream(stream);
+    if (dim % 4 == 0 && aligned16(pos_table) && aligned16(embeddings))
+        hipLaunchKernelGGL(pos_add_kernel<4>, grid, block, 0, st, pos_table, embeddings,
+                           static_cast<int>(rows), seq, dim);
+    else
+        hipLaunchKernelGGL(pos_add_kernel<1>, grid, block, 0, st, pos_table, embeddings,
+                           static_cast<int>(rows), seq, dim);
+    return check_launch(name);
+}
+
+int mi_pos_embedding_backward(const float* grad_out, float* grad_pos_table, int batch, int seq,
+                              int dim, void* stream) {
+    const char* name = "mi_pos_embedding_backward";
+    if (batch < 0 || seq <= 0 || dim <= 0)
+        return set_error(MI_ERR_INVALID_ARG, "%s: batch=%d seq=%d dim=%d", name, batch, seq, dim);
+    if (batch == 0) return MI_OK;
+    if (!grad_out || !grad_pos_table) return set_error(MI_ERR_INVALID_ARG, "%s: NULL", name);
+    hipStream_t st = to_stream(stream);
+    const bool v4 = dim % 4 == 0 && aligned16(grad_out) && aligned16(grad_pos_table);
+    const long long threads = static_cast<long long>(seq) * (v4 ? dim / 4 : dim);
+    const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+    if (v4)
+        hipLaunchKernelGGL(pos_bwd_kernel<4>, grid, dim3(256), 0, st, grad_out, grad_pos_table,
+                           batch, seq, dim);
+    else
+        hipLaunchKernelGGL(pos_bwd_kernel<1>, grid, dim3(256), 0, st, grad_out, grad_pos_table,
+                           batch, seq, dim);
+    return check_launch(name);
+}
+
+int mi_embedding_backward(const float* grad_out, const int* tokens, float* grad_table,
+                          int batch_seq, int dim, int vocab, void* stream) {
+    const char* name = "mi_embedding_backward";
+    if (batch_seq < 0 || dim <= 0)
+        return set_error(MI_ERR_INVALID_ARG, "%s: batch_seq=%d dim=%d", name, batch_seq, dim);
+    if (batch_seq == 0) return MI_OK;
+    if (!grad_out || !tokens || !grad_table) return set_error(MI_ERR_INVALID_ARG, "%s: NULL", name);
+    hipStream_t st = to_stream(stream);
+    const SortPlan p = plan_sort(batch_seq, vocab);
+    int err = MI_OK;
+    char* ws = static_cast<char*>(workspace_get(p.bytes, st, &err));
+    if (!ws) return err;
+    unsigned* k[2] = {reinterpret_cast<unsigned*>(ws), reinterpret_cast<unsigned*>(ws + p.off_k1)};
+    int* v[2] = {reinterpret_cast<int*>(ws + p.off_v0), reinterpret_cast<int*>(ws + p.off_v1)};
+    int* hist = reinterpret_cast<int*>(ws + p.off_hist);
+    const int n = batch_seq;
+
+    hipLaunchKernelGGL(prep_keys_kernel, dim3((n + 255) / 256), dim3(256), 0, st, tokens, k[0],
+                       v[0], n, vocab);
+    int cur = 0;
+    for (int pass = 0; pass < p.passes; ++pass) {
+        const int shift = 8 * pass;
+        hipLaunchKernelGGL(radix_hist_kernel, dim3(p.ntiles), dim3(256), 0, st, k[cur], n, shift,
+                           p.ntiles, hist);
+        hipLaunchKernelGGL(exclusive_scan_kernel, dim3(1), dim3(1024), 0, st, hist,
+                           p.ntiles * kDigits);
+        hipLaunchKernelGGL(radix_scatter_kernel, dim3(p.ntiles), dim3(kWave), 0, st, k[cur],
+                           v[cur], k[cur ^ 1], v[cur ^ 1], n, shift, p.ntiles, hist);
+        cur ^= 1;
+    }
+    const dim3 grid((n + kRowWaves - 1) / kRowWaves), block(kRowWaves * kWave);
+    if (dim % 4 == 0 && aligned16(grad_out) && aligned16(grad_table))
+        hipLaunchKernelGGL((emb_bwd_accum_kernel<4, 4>), grid, block, 0, st, k[cur], v[cur], n,
+                           grad_out, grad_table, dim);
+    else
+        hipLaunchKernelGGL((emb_bwd_accum_kernel<1, 4>), grid, block, 0, st, k[cur], v[cur], n,
+                           grad_out, grad_table, dim);
+    return check_launch(name);
+}
+
+}  // extern "C"

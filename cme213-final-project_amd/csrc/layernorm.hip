@@ -1,0 +1,584 @@
+// LayerNorm forward / backward for gfx950.
+//
+// Reference behaviour: FINAL_CLEAN_CODE/src/kernels/layernorm.cu.  The
+// reference runs one 256-thread block per row and walks the row three times
+// from global memory (sum, variance, normalise); the backward re-reads
+// grad_out and x a second time, column-strided, for dgamma / dbeta.
+//
+// Here:
+//  * forward: one wave64 per row, the row held in registers as W-wide
+//    vectors (W = 4 -> global_load_dwordx4), so x is read from HBM once;
+//    mean and variance are two wave reductions over the registers.
+//  * backward: a "row group" of G waves owns a row (G = 1 up to 2048
+//    columns, 4 beyond); grad_out and x are read once per row.  dx is
+//    written in the same pass, and each thread keeps running dgamma/dbeta
+//    sums for the columns it owns across all rows its group visits.  At the
+//    end the groups of a workgroup combine through LDS (fixed tree) and the
+//    workgroup writes one partial row; colsum_finalize adds the partial
+//    rows in a fixed order.  No float atomics: bitwise reproducible.
+//  * rows wider than the register-resident templates fall back to
+//    block-per-row kernels that stream the row from global memory.
+#include <climits>
+
+#include "mi_common.hpp"
+
+#ifndef MI_LN_BWD_MAX_BLOCKS
+#define MI_LN_BWD_MAX_BLOCKS 512
+#endif
+
+namespace mi {
+
+namespace {
+
+constexpr int kFwdWaves = 4;      // rows (waves) per forward workgroup
+constexpr int kBwdWaves = 8;      // waves per backward workgroup
+constexpr int kBlockThreads = 256;  // generic block-per-row kernels
+
+// ---------------------------------------------------------------------------
+// Forward, one wave per row.
+// ---------------------------------------------------------------------------
+template <int W, int N, bool SAVE, bool RESID>
+__global__ __launch_bounds__(kFwdWaves * kWave) void ln_fwd_wave_kernel(
+    const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float* __restrict__ resid_out, float* __restrict__ out,
+    float* __restrict__ mean_out, float* __restrict__ rstd_out, int rows, int cols, float eps) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int row = blockIdx.x * kFwdWaves + static_cast<int>(threadIdx.x / kWave);
+    if (row >= rows) return;  // wave-uniform
+    const int nv = cols / W;
+    const size_t base = static_cast<size_t>(row) * cols;
+
+    fvec<W> v[N];
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        const int j = lane + k * kWave;
+        if (j < nv) {
+            v[k] = vload<W>(a + base, j);
+            if constexpr (RESID) {
+                const fvec<W> w = vload<W>(b + base, j);
+#pragma unroll
+                for (int e = 0; e < W; ++e) v[k].v[e] = v[k].v[e] + w.v[e];
+                vstore<W>(resid_out + base, j, v[k]);
+            }
+        } else {
+            v[k] = vzero<W>();
+        }
+    }
+
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < N; ++k)
+#pragma unroll
+        for (int e = 0; e < W; ++e) s += v[k].v[e];
+    const float mean = wave_sum(s) / static_cast<float>(cols);
+
+    float q = 0.0f;
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        const bool ok = (lane + k * kWave) < nv;
+#pragma unroll
+        for (int e = 0; e < W; ++e) {
+            const float d = ok ? (v[k].v[e] - mean) : 0.0f;
+            q += d * d;
+        }
+    }
+    const float var = wave_sum(q) / static_cast<float>(cols);
+    const float rstd = 1.0f / sqrtf(var + eps);
+    if constexpr (SAVE) {
+        if (lane == 0) {
+            mean_out[row] = mean;
+            rstd_out[row] = rstd;
+        }
+    }
+
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        const int j = lane + k * kWave;
+        if (j < nv) {
+            const fvec<W> g = vload<W>(gamma, j);
+            const fvec<W> bt = vload<W>(beta, j);
+            fvec<W> y;
+#pragma unroll
+            for (int e = 0; e < W; ++e) y.v[e] = (v[k].v[e] - mean) * rstd * g.v[e] + bt.v[e];
+            vstore<W>(out + base, j, y);
+        }
+    }
+}
+
+// Sum over the block; every thread returns the same value.  `red` holds one
+// float per wave.
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    const float w = wave_sum(v);
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = w;
+    __syncthreads();
+    float t = red[0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) t += red[i];
+    __syncthreads();
+    return t;
+}
+
+// Forward, one block per row, any width (streams the row three times).
+template <bool SAVE, bool RESID>
+__global__ __launch_bounds__(kBlockThreads) void ln_fwd_block_kernel(
+    const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float* __restrict__ resid_out, float* __restrict__ out,
+    float* __restrict__ mean_out, float* __restrict__ rstd_out, int rows, int cols, float eps) {
+    constexpr int NW = kBlockThreads / kWave;
+    __shared__ float red[NW];
+    const int row = blockIdx.x;
+    const size_t base = static_cast<size_t>(row) * cols;
+    const float* src = RESID ? resid_out + base : a + base;
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < cols; i += kBlockThreads) {
+        float r = a[base + i];
+        if constexpr (RESID) {
+            r = r + b[base + i];
+            resid_out[base + i] = r;  // re-read below by this same thread
+        }
+        s += r;
+    }
+    const float mean = block_sum<NW>(s, red) / static_cast<float>(cols);
+    float q = 0.0f;
+    for (int i = threadIdx.x; i < cols; i += kBlockThreads) {
+        const float d = src[i] - mean;
+        q += d * d;
+    }
+    const float var = block_sum<NW>(q, red) / static_cast<float>(cols);
+    const float rstd = 1.0f / sqrtf(var + eps);
+    if constexpr (SAVE) {
+        if (threadIdx.x == 0) {
+            mean_out[row] = mean;
+            rstd_out[row] = rstd;
+        }
+    }
+    for (int i = threadIdx.x; i < cols; i += kBlockThreads)
+        out[base + i] = (src[i] - mean) * rstd * gamma[i] + beta[i];
+}
+
+// ---------------------------------------------------------------------------
+// Backward, G waves per row, kBwdWaves waves per workgroup.
+// Dynamic LDS: (GPB/2) slots of 2*N*W*64*G floats for the final combine.
+// ---------------------------------------------------------------------------
+template <int W, int N, int G, bool ADD>
+__global__ __launch_bounds__(kBwdWaves * kWave) void ln_bwd_group_kernel(
+    const float* __restrict__ gout, const float* __restrict__ x, const float* __restrict__ mean,
+    const float* __restrict__ rstd, const float* __restrict__ gamma, float* __restrict__ gx,
+    float* __restrict__ part, int rows, int cols) {
+    constexpr int GPB = kBwdWaves / G;  // row groups per workgroup
+    constexpr int GT = G * kWave;       // threads per group
+    extern __shared__ float lds[];
+    __shared__ float red[2][kBwdWaves][2];
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int grp = wave / G;
+    const int wig = wave % G;
+    const int t = wig * kWave + lane;
+    const int nv = cols / W;
+
+    fvec<W> gm[N], ag[N], ab[N];
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        const int j = t + k * GT;
+        gm[k] = (j < nv) ? vload<W>(gamma, j) : vzero<W>();
+        ag[k] = vzero<W>();
+        ab[k] = vzero<W>();
+    }
+
+    const int stride = gridDim.x * GPB;
+    int it = 0;
+    // The trip count is uniform across the workgroup (groups past the last
+    // row idle through the iteration) so the barriers below are reached by
+    // every wave.
+    for (int base_row = blockIdx.x * GPB; base_row < rows; base_row += stride, ++it) {
+        const int row = base_row + grp;
+        const bool valid = row < rows;
+        const size_t off = static_cast<size_t>(valid ? row : 0) * cols;
+        fvec<W> go[N], xv[N];
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            const int j = t + k * GT;
+            const bool ok = valid && j < nv;
+            go[k] = ok ? vload<W>(gout + off, j) : vzero<W>();
+            xv[k] = ok ? vload<W>(x + off, j) : vzero<W>();
+        }
+        const float mu = valid ? mean[row] : 0.0f;
+        const float is = valid ? rstd[row] : 0.0f;
+
+        float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < N; ++k)
+#pragma unroll
+            for (int e = 0; e < W; ++e) {
+                const float xh = (xv[k].v[e] - mu) * is;
+                const float dh = go[k].v[e] * gm[k].v[e];
+                s1 += dh;
+                s2 += dh * xh;
+            }
+        // Masked slots hold go = 0, so they add exact zeros to s1 and s2.
+        float S1 = wave_sum(s1);
+        float S2 = wave_sum(s2);
+        if constexpr (G > 1) {
+            float(*r)[2] = red[it & 1];
+            if (lane == 0) {
+                r[wave][0] = S1;
+                r[wave][1] = S2;
+            }
+            __syncthreads();
+            const int w0 = grp * G;
+            S1 = r[w0][0];
+            S2 = r[w0][1];
+#pragma unroll
+            for (int i = 1; i < G; ++i) {
+                S1 += r[w0 + i][0];
+                S2 += r[w0 + i][1];
+            }
+            // red is double-buffered by iteration parity, so the next
+            // iteration's writes cannot race these reads.
+        }
+        const float m1 = S1 / static_cast<float>(cols);
+        const float m2 = S2 / static_cast<float>(cols);
+
+        if (valid) {
+#pragma unroll
+            for (int k = 0; k < N; ++k) {
+                const int j = t + k * GT;
+                if (j < nv) {
+                    fvec<W> d;
+                    if constexpr (ADD) d = vload<W>(gx + off, j);
+#pragma unroll
+                    for (int e = 0; e < W; ++e) {
+                        const float xh = (xv[k].v[e] - mu) * is;
+                        const float dh = go[k].v[e] * gm[k].v[e];
+                        const float dx = is * (dh - m1 - xh * m2);
+                        if constexpr (ADD)
+                            d.v[e] = d.v[e] + dx;
+                        else
+                            d.v[e] = dx;
+                        ag[k].v[e] += go[k].v[e] * xh;
+                        ab[k].v[e] += go[k].v[e];
+                    }
+                    vstore<W>(gx + off, j, d);
+                }
+            }
+        }
+    }
+
+    // Combine the GPB groups' running sums: a fixed binary tree through LDS.
+    constexpr int SLOT = 2 * N * W * GT;
+#pragma unroll
+    for (int h = GPB / 2; h >= 1; h /= 2) {
+        if (grp >= h && grp < 2 * h) {
+            float* s = lds + (grp - h) * SLOT;
+#pragma unroll
+            for (int k = 0; k < N; ++k)
+#pragma unroll
+                for (int e = 0; e < W; ++e) {
+                    s[((0 * N + k) * W + e) * GT + t] = ag[k].v[e];
+                    s[((1 * N + k) * W + e) * GT + t] = ab[k].v[e];
+                }
+        }
+        __syncthreads();
+        if (grp < h) {
+            const float* s = lds + grp * SLOT;
+#pragma unroll
+            for (int k = 0; k < N; ++k)
+#pragma unroll
+                for (int e = 0; e < W; ++e) {
+                    ag[k].v[e] += s[((0 * N + k) * W + e) * GT + t];
+                    ab[k].v[e] += s[((1 * N + k) * W + e) * GT + t];
+                }
+        }
+        __syncthreads();
+    }
+    if (grp == 0) {
+        float* pg = part + static_cast<size_t>(blockIdx.x) * 2 * cols;
+        float* pb = pg + cols;
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            const int j = t + k * GT;
+            if (j < nv) {
+                vstore<W>(pg, j, ag[k]);
+                vstore<W>(pb, j, ab[k]);
+            }
+        }
+    }
+}
+
+// Backward, one block per row group, any width.  Each thread owns columns
+// c = tid + i*256 and keeps its dgamma/dbeta running sums directly in the
+// block's partial row (only this block touches it, so plain loads/stores).
+template <bool ADD>
+__global__ __launch_bounds__(kBlockThreads) void ln_bwd_block_kernel(
+    const float* __restrict__ gout, const float* __restrict__ x, const float* __restrict__ mean,
+    const float* __restrict__ rstd, const float* __restrict__ gamma, float* __restrict__ gx,
+    float* __restrict__ part, int rows, int cols) {
+    constexpr int NW = kBlockThreads / kWave;
+    __shared__ float red[NW];
+    float* pg = part + static_cast<size_t>(blockIdx.x) * 2 * cols;
+    float* pb = pg + cols;
+    for (int c = threadIdx.x; c < cols; c += kBlockThreads) {
+        pg[c] = 0.0f;
+        pb[c] = 0.0f;
+    }
+    for (int row = blockIdx.x; row < rows; row += gridDim.x) {
+        const size_t off = static_cast<size_t>(row) * cols;
+        const float mu = mean[row];
+        const float is = rstd[row];
+        float s1 = 0.0f, s2 = 0.0f;
+        for (int c = threadIdx.x; c < cols; c += kBlockThreads) {
+            const float xh = (x[off + c] - mu) * is;
+            const float dh = gout[off + c] * gamma[c];
+            s1 += dh;
+            s2 += dh * xh;
+        }
+        const float m1 = block_sum<NW>(s1, red) / static_cast<float>(cols);
+        const float m2 = block_sum<NW>(s2, red) / static_cast<float>(cols);
+        for (int c = threadIdx.x; c < cols; c += kBlockThreads) {
+            const float g = gout[off + c];
+            const float xh = (x[off + c] - mu) * is;
+            const float dh = g * gamma[c];
+            const float dx = is * (dh - m1 - xh * m2);
+            if constexpr (ADD)
+                gx[off + c] = gx[off + c] + dx;
+            else
+                gx[off + c] = dx;
+            pg[c] = pg[c] + g * xh;
+            pb[c] = pb[c] + g;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host dispatch.
+// ---------------------------------------------------------------------------
+
+// Smallest supported vectors-per-lane count >= need, or 0 if none.
+int pick_n(int need) {
+    static const int kN[] = {1, 2, 3, 4, 6, 8, 12, 16};
+    for (int n : kN)
+        if (n >= need) return n;
+    return 0;
+}
+
+template <int W, bool SAVE, bool RESID>
+void launch_fwd_wave(int n, dim3 grid, hipStream_t st, const float* a, const float* b,
+                     const float* gamma, const float* beta, float* ro, float* out, float* mo,
+                     float* so, int rows, int cols, float eps) {
+    const dim3 block(kFwdWaves * kWave);
+#define MI_LN_FWD_CASE(NN)                                                                  \
+    case NN:                                                                                \
+        hipLaunchKernelGGL((ln_fwd_wave_kernel<W, NN, SAVE, RESID>), grid, block, 0, st, a, \
+                           b, gamma, beta, ro, out, mo, so, rows, cols, eps);               \
+        break;
+    switch (n) {
+        MI_LN_FWD_CASE(1)
+        MI_LN_FWD_CASE(2)
+        MI_LN_FWD_CASE(3)
+        MI_LN_FWD_CASE(4)
+        MI_LN_FWD_CASE(6)
+        MI_LN_FWD_CASE(8)
+        MI_LN_FWD_CASE(12)
+        MI_LN_FWD_CASE(16)
+        default:
+            break;
+    }
+#undef MI_LN_FWD_CASE
+}
+
+template <bool SAVE, bool RESID>
+int ln_forward_impl(const char* name, const float* a, const float* b, const float* gamma,
+                    const float* beta, float* ro, float* out, float* mo, float* so, int rows,
+                    int cols, float eps, hipStream_t st) {
+    if (rows < 0 || cols <= 0)
+        return set_error(MI_ERR_INVALID_ARG, "%s: invalid shape rows=%d cols=%d", name, rows,
+                         cols);
+    if (rows == 0) return MI_OK;
+    if (!a || !gamma || !beta || !out || (RESID && (!b || !ro)) || (SAVE && (!mo || !so)))
+        return set_error(MI_ERR_INVALID_ARG, "%s: NULL pointer", name);
+    const bool vec4 = (cols % 4 == 0) && aligned16(a) && aligned16(gamma) && aligned16(beta) &&
+                      aligned16(out) && (!RESID || (aligned16(b) && aligned16(ro)));
+    const int W = vec4 ? 4 : 1;
+    const int need = (cols / W + kWave - 1) / kWave;
+    const int n = pick_n(need);
+    if (n != 0) {
+        const dim3 grid((rows + kFwdWaves - 1) / kFwdWaves);
+        if (vec4)
+            launch_fwd_wave<4, SAVE, RESID>(n, grid, st, a, b, gamma, beta, ro, out, mo, so, rows,
+                                            cols, eps);
+        else
+            launch_fwd_wave<1, SAVE, RESID>(n, grid, st, a, b, gamma, beta, ro, out, mo, so, rows,
+                                            cols, eps);
+    } else {
+        hipLaunchKernelGGL((ln_fwd_block_kernel<SAVE, RESID>), dim3(rows), dim3(kBlockThreads), 0,
+                           st, a, b, gamma, beta, ro, out, mo, so, rows, cols, eps);
+    }
+    return check_launch(name);
+}
+
+struct BwdPlan {
+    int W = 1, N = 0, G = 1;  // N == 0: block-per-row fallback
+    int blocks = 0;
+    size_t lds = 0;
+};
+
+BwdPlan plan_bwd(int rows, int cols, bool vec4) {
+    BwdPlan p;
+    p.W = vec4 ? 4 : 1;
+    const int nv = cols / p.W;
+    // (G, largest N) pairs keep the combine LDS at or under 48 KB:
+    // G = 1: 4 slots of 2*N*W*64 floats; G = 4: 1 slot of 2*N*W*256 floats;
+    // G = 8: one group per workgroup, no combine.
+    static const int kG[] = {1, 4, 8};
+    static const int kMaxN[] = {6, 6, 8};
+    static const int kN[] = {1, 2, 3, 4, 6, 8};
+    for (int gi = 0; gi < 3 && !p.N; ++gi) {
+        const int g = kG[gi];
+        const int need = (nv + g * kWave - 1) / (g * kWave);
+        for (int n : kN)
+            if (n >= need && n <= kMaxN[gi]) {
+                p.N = n;
+                p.G = g;
+                break;
+            }
+    }
+    if (p.N) {
+        const int gpb = kBwdWaves / p.G;
+        const long long groups = (rows + gpb - 1) / gpb;
+        p.blocks = static_cast<int>(groups < MI_LN_BWD_MAX_BLOCKS ? groups : MI_LN_BWD_MAX_BLOCKS);
+        p.lds = static_cast<size_t>(gpb / 2) * 2 * p.N * p.W * p.G * kWave * sizeof(float);
+    } else {
+        p.blocks = rows < MI_LN_BWD_MAX_BLOCKS ? rows : MI_LN_BWD_MAX_BLOCKS;
+    }
+    if (p.blocks < 1) p.blocks = 1;
+    return p;
+}
+
+template <int W, int N, int G, bool ADD>
+void launch_bwd_group(const BwdPlan& p, hipStream_t st, const float* g, const float* x,
+                      const float* m, const float* s, const float* gamma, float* gx, float* part,
+                      int rows, int cols) {
+    hipLaunchKernelGGL((ln_bwd_group_kernel<W, N, G, ADD>), dim3(p.blocks),
+                       dim3(kBwdWaves * kWave), p.lds, st, g, x, m, s, gamma, gx, part, rows,
+                       cols);
+}
+
+template <int W, int G, bool ADD>
+void dispatch_bwd_n(const BwdPlan& p, hipStream_t st, const float* g, const float* x,
+                    const float* m, const float* s, const float* gamma, float* gx, float* part,
+                    int rows, int cols) {
+    switch (p.N) {
+        case 1: launch_bwd_group<W, 1, G, ADD>(p, st, g, x, m, s, gamma, gx, part, rows, cols); break;
+        case 2: launch_bwd_group<W, 2, G, ADD>(p, st, g, x, m, s, gamma, gx, part, rows, cols); break;
+        case 3: launch_bwd_group<W, 3, G, ADD>(p, st, g, x, m, s, gamma, gx, part, rows, cols); break;
+        case 4: launch_bwd_group<W, 4, G, ADD>(p, st, g, x, m, s, gamma, gx, part, rows, cols); break;
+        case 6: launch_bwd_group<W, 6, G, ADD>(p, st, g, x, m, s, gamma, gx, part, rows, cols); break;
+        case 8: launch_bwd_group<W, 8, G, ADD>(p, st, g, x, m, s, gamma, gx, part, rows, cols); break;
+        default: break;
+    }
+}
+
+template <int W, bool ADD>
+void dispatch_bwd_g(const BwdPlan& p, hipStream_t st, const float* g, const float* x,
+                    const float* m, const float* s, const float* gamma, float* gx, float* part,
+                    int rows, int cols) {
+    switch (p.G) {
+        case 1: dispatch_bwd_n<W, 1, ADD>(p, st, g, x, m, s, gamma, gx, part, rows, cols); break;
+        case 4: dispatch_bwd_n<W, 4, ADD>(p, st, g, x, m, s, gamma, gx, part, rows, cols); break;
+        case 8: dispatch_bwd_n<W, 8, ADD>(p, st, g, x, m, s, gamma, gx, part, rows, cols); break;
+        default: break;
+    }
+}
+
+size_t bwd_workspace(const BwdPlan& p, int cols) {
+    return static_cast<size_t>(p.blocks) * 2 * static_cast<size_t>(cols) * sizeof(float);
+}
+
+template <bool ADD>
+int ln_backward_impl(const char* name, const float* g, const float* x, const float* m,
+                     const float* s, const float* gamma, float* gx, float* dgamma, float* dbeta,
+                     int rows, int cols, hipStream_t st) {
+    if (rows < 0 || cols <= 0)
+        return set_error(MI_ERR_INVALID_ARG, "%s: invalid shape rows=%d cols=%d", name, rows,
+                         cols);
+    if (rows == 0) return MI_OK;
+    if (!g || !x || !m || !s || !gamma || !gx || !dgamma || !dbeta)
+        return set_error(MI_ERR_INVALID_ARG, "%s: NULL pointer", name);
+    const bool vec4 = (cols % 4 == 0) && aligned16(g) && aligned16(x) && aligned16(gamma) &&
+                      aligned16(gx);
+    const BwdPlan p = plan_bwd(rows, cols, vec4);
+    int err = MI_OK;
+    float* part = static_cast<float*>(workspace_get(bwd_workspace(p, cols), st, &err));
+    if (!part) return err;
+    if (p.N) {
+        if (p.W == 4)
+            dispatch_bwd_g<4, ADD>(p, st, g, x, m, s, gamma, gx, part, rows, cols);
+        else
+            dispatch_bwd_g<1, ADD>(p, st, g, x, m, s, gamma, gx, part, rows, cols);
+    } else {
+        hipLaunchKernelGGL((ln_bwd_block_kernel<ADD>), dim3(p.blocks), dim3(kBlockThreads), 0, st,
+                           g, x, m, s, gamma, gx, part, rows, cols);
+    }
+    int rc = check_launch(name);
+    if (rc != MI_OK) return rc;
+    return launch_colsum_finalize(part, p.blocks, 2 * cols, dgamma, cols, dbeta, st);
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" {
+
+size_t mi_layernorm_backward_workspace(int rows, int cols) {
+    if (rows <= 0 || cols <= 0) return 0;
+    // The vec4 and scalar plans can differ; report the larger.
+    const size_t a = bwd_workspace(plan_bwd(rows, cols, cols % 4 == 0), cols);
+    const size_t b = bwd_workspace(plan_bwd(rows, cols, false), cols);
+    return a > b ? a : b;
+}
+
+int mi_layernorm_forward(const float* x, const float* gamma, const float* beta, float* out,
+                         int rows, int cols, float eps, void* stream) {
+    return ln_forward_impl<false, false>("mi_layernorm_forward", x, nullptr, gamma, beta, nullptr,
+                                         out, nullptr, nullptr, rows, cols, eps,
+                                         to_stream(stream));
+}
+
+int mi_layernorm_forward_save(const float* x, const float* gamma, const float* beta, float* out,
+                              float* mean, float* inv_std, int rows, int cols, float eps,
+                              void* stream) {
+    return ln_forward_impl<true, false>("mi_layernorm_forward_save", x, nullptr, gamma, beta,
+                                        nullptr, out, mean, inv_std, rows, cols, eps,
+                                        to_stream(stream));
+}
+
+int mi_residual_layernorm_forward_save(const float* a, const float* b, const float* gamma,
+                                       const float* beta, float* residual_out, float* out,
+                                       float* mean, float* inv_std, int rows, int cols, float eps,
+                                       void* stream) {
+    return ln_forward_impl<true, true>("mi_residual_layernorm_forward_save", a, b, gamma, beta,
+                                       residual_out, out, mean, inv_std, rows, cols, eps,
+                                       to_stream(stream));
+}
+
+int mi_layernorm_backward(const float* grad_out, const float* x, const float* mean,
+                          const float* inv_std, const float* gamma, float* grad_x, float* dgamma,
+                          float* dbeta, int rows, int cols, void* stream) {
+    return ln_backward_impl<false>("mi_layernorm_backward", grad_out, x, mean, inv_std, gamma,
+                                   grad_x, dgamma, dbeta, rows, cols, to_stream(stream));
+}
+
+int mi_layernorm_backward_residual(const float* grad_out, const float* x, const float* mean,
+                                   const float* inv_std, const float* gamma, float* grad_residual,
+                                   float* dgamma, float* dbeta, int rows, int cols,
+                                   void* stream) {
+    return ln_backward_impl<true>("mi_layernorm_backward_residual", grad_out, x, mean, inv_std,
+                                  gamma, grad_residual, dgamma, dbeta, rows, cols,
+                                  to_stream(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,100 @@
+// Shared device helpers and host plumbing for the gfx950 layer kernels.
+//
+// Device side: wave64 reductions built from DPP row operations plus
+// v_readlane, 4-wide vector load/store types, and the launch-shape
+// constants.  Host side: the error slot returned through mi_last_error(),
+// stream conversion, and the per-device workspace used by the deterministic
+// two-pass column reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "mi_kernels.h"
+
+namespace mi {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// Vector types.  fvec<4> is 16-byte aligned so a load through it becomes one
+// global_load_dwordx4; fvec<1> is the scalar fallback for widths that are not
+// a multiple of 4 or pointers that are not 16-byte aligned.
+// ---------------------------------------------------------------------------
+template <int W>
+struct alignas(4 * W) fvec {
+    float v[W];
+};
+
+template <int W>
+__device__ __forceinline__ fvec<W> vzero() {
+    fvec<W> r;
+#pragma unroll
+    for (int e = 0; e < W; ++e) r.v[e] = 0.0f;
+    return r;
+}
+
+template <int W>
+__device__ __forceinline__ fvec<W> vload(const float* base, size_t vec_index) {
+    return reinterpret_cast<const fvec<W>*>(base)[vec_index];
+}
+
+template <int W>
+__device__ __forceinline__ void vstore(float* base, size_t vec_index, const fvec<W>& x) {
+    reinterpret_cast<fvec<W>*>(base)[vec_index] = x;
+}
+
+// ---------------------------------------------------------------------------
+// Wave64 sum.  Four DPP steps reduce each 16-lane row (quad xor-1, quad
+// xor-2, half-row mirror, row mirror); the four row totals are then read
+// with v_readlane and added in a fixed order.  Every lane returns the same
+// bit pattern, and the association order is fixed by the code, so the
+// result is deterministic.  All 64 lanes must be active at the call.
+// ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __int_as_float(
+        __builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float readlane(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
+    v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
+    v += dpp_move<0x141>(v);  // row_half_mirror: 8-lane groups
+    v += dpp_move<0x140>(v);  // row_mirror: 16-lane rows
+    const float r0 = readlane(v, 0);
+    const float r1 = readlane(v, 16);
+    const float r2 = readlane(v, 32);
+    const float r3 = readlane(v, 48);
+    return (r0 + r1) + (r2 + r3);
+}
+
+// ---------------------------------------------------------------------------
+// Host plumbing (defined in runtime.hip).
+// ---------------------------------------------------------------------------
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+inline hipStream_t to_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Returns a device buffer of at least `bytes` for the current device (the
+// library-owned workspace), growing it if needed.  Growth is refused while
+// `stream` is being captured into a graph.  On failure returns nullptr and
+// stores the error code in *err.
+void* workspace_get(size_t bytes, hipStream_t stream, int* err);
+
+// out0[c] += sum_p part[p * ncols + c] for c < split, out1[c - split] for
+// c >= split; fixed summation order (reduce.hip).
+int launch_colsum_finalize(const float* part, int P, int ncols, float* out0, int split,
+                           float* out1, hipStream_t stream);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace mi

@@ -1,0 +1,91 @@
+// kernels.h — drop-in C++ interface for the reference's fused non-GEMM
+// layer path, implemented by the gfx950 library (libcme213_amd.so).
+//
+// The declarations below have exactly the signatures, default arguments and
+// semantics of the hot-path subset of the reference's
+// FINAL_CLEAN_CODE/include/kernels.h (line numbers cited per group), so the
+// reference's callers (FINAL_CLEAN_CODE/src/model/transformer.cu:337-408,
+// :421-590 and its tests) compile against this header unchanged for these
+// calls.  As in the reference, every call launches asynchronously on the
+// calling thread's default stream (hipStreamPerThread, the HIP counterpart
+// of nvcc --default-stream per-thread) and returns void; a failure prints
+// "HIP error at <file>:<line> — <message>" and calls exit(EXIT_FAILURE),
+// mirroring CUDA_CHECK_LAST (FINAL_CLEAN_CODE/include/common.h:20-30).
+//
+// Differences in behaviour, all deliberate:
+//  * dgamma/dbeta, dbias and the embedding gradients are computed with a
+//    deterministic two-pass reduction instead of float atomics, so results
+//    are bitwise reproducible;
+//  * embedding_backward accumulates each table row in increasing token
+//    position, which makes it bit-identical to the reference's CPU loop.
+// The same kernels are reachable through the C ABI in mi_kernels.h.
+#pragma once
+
+#include "mi_kernels.h"
+
+// --- LayerNorm (reference kernels.h:53-76) ---------------------------------
+void layernorm_forward(const float* x, const float* gamma, const float* beta,
+                       float* out, int rows, int cols, float eps = 1e-5f);
+
+void layernorm_forward_save(const float* x, const float* gamma, const float* beta,
+                            float* out, float* mean, float* inv_std,
+                            int rows, int cols, float eps = 1e-5f);
+
+void residual_layernorm_forward_save(const float* a, const float* b,
+                                     const float* gamma, const float* beta,
+                                     float* residual_out, float* out,
+                                     float* mean, float* inv_std,
+                                     int rows, int cols, float eps = 1e-5f);
+
+void layernorm_backward(const float* grad_out, const float* x,
+                        const float* mean, const float* inv_std,
+                        const float* gamma,
+                        float* grad_x, float* dgamma, float* dbeta,
+                        int rows, int cols);
+
+void layernorm_backward_residual(const float* grad_out, const float* x,
+                                 const float* mean, const float* inv_std,
+                                 const float* gamma,
+                                 float* grad_residual, float* dgamma, float* dbeta,
+                                 int rows, int cols);
+
+// --- ReLU, residual (reference kernels.h:78-92) ----------------------------
+void relu_forward(const float* in, float* out, int n);
+void relu_backward(const float* in, const float* grad_out, float* grad_in, int n);
+
+void relu_backward_with_bias_backward(const float* mask, const float* grad_out,
+                                      float* grad_in, float* dbias,
+                                      int rows, int cols);
+
+void residual_add(const float* a, const float* b, float* out, int n);
+
+void residual_add_with_bias(const float* residual, const float* x,
+                            const float* bias, float* out,
+                            int rows, int cols);
+
+// --- bias (reference kernels.h:104-111) -------------------------------------
+void bias_add(float* out, const float* bias, int rows, int cols);
+
+void bias_relu_forward(const float* in, const float* bias, float* out,
+                       int rows, int cols);
+
+void bias_backward(const float* grad, float* dbias, int rows, int cols);
+
+// --- bias + tanh-GELU: new operators in the reference's naming style, for
+// the slots of bias_relu_forward and relu_backward_with_bias_backward. ------
+void bias_gelu_forward(const float* in, const float* bias, float* out,
+                       int rows, int cols);
+
+void gelu_backward_with_bias_backward(const float* in, const float* bias,
+                                      const float* grad_out, float* grad_in,
+                                      float* dbias, int rows, int cols);
+
+// --- embedding (reference kernels.h:131-138) -------------------------------
+void embedding_forward(const float* table, const int* tokens,
+                       float* out, int batch_seq, int dim);
+void embedding_backward(const float* grad_out, const int* tokens,
+                        float* grad_table, int batch_seq, int dim);
+void pos_embedding_forward(const float* pos_table, float* embeddings,
+                           int batch, int seq, int dim);
+void pos_embedding_backward(const float* grad_out, float* grad_pos_table,
+                            int batch, int seq, int dim);

@@ -1,0 +1,192 @@
+/*
+ * mi_kernels.h — C ABI of the MI355X (gfx950) fused non-GEMM layer kernels.
+ *
+ * Every compute entry point replaces one free function of the reference's
+ * C++ kernel interface, FINAL_CLEAN_CODE/include/kernels.h (cited per
+ * function as kernels.h:line), with the same argument meaning, the same
+ * overwrite-versus-accumulate contract and the same aliasing rules.  The
+ * differences are the ones a C ABI needs:
+ *
+ *  - C linkage and an "mi_" prefix (the C++ names with the reference's exact
+ *    signatures live in kernels.h of this directory and forward here);
+ *  - an explicit stream (a hipStream_t passed as void*; NULL = the legacy
+ *    default stream);
+ *  - an int status instead of exit(): 0 on success, a hipError_t value for
+ *    a runtime failure, or one of the MI_ERR_* codes below; mi_last_error()
+ *    returns the message of the most recent failure on the calling thread.
+ *
+ * All pointers are device pointers owned by the caller, fp32 row-major
+ * contiguous (ids int32).  Calls are asynchronous on `stream` and perform no
+ * host synchronisation.  The column reductions (dgamma/dbeta/dbias, the
+ * embedding gradients) are deterministic: two-pass, no float atomics, so
+ * repeated calls on identical inputs give identical bits.  Those entry points
+ * use a library-owned device workspace; it is allocated on first use (or by
+ * mi_workspace_reserve) and may not grow while the stream is being captured
+ * into a graph.  Calls that share the workspace must not run concurrently on
+ * different streams of the same device.
+ */
+#ifndef MI_KERNELS_H
+#define MI_KERNELS_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MI_OK 0
+#define MI_ERR_INVALID_ARG (-1)    /* bad size, NULL pointer, unsupported shape */
+#define MI_ERR_CAPTURE_ALLOC (-2)  /* workspace growth needed during capture */
+
+/* ----- runtime helpers (so a ctypes driver needs no other library) ------ */
+
+const char* mi_last_error(void);
+const char* mi_version(void);
+int mi_device_count(int* count);
+int mi_set_device(int device);
+int mi_malloc(void** ptr, size_t bytes);
+int mi_free(void* ptr);
+int mi_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int mi_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int mi_memset_zero(void* ptr, size_t bytes, void* stream);
+int mi_stream_sync(void* stream);
+int mi_device_sync(void);
+/* Grow the library workspace of the current device to >= bytes now (call
+ * before graph capture).  mi_workspace_bytes() reports its current size. */
+int mi_workspace_reserve(size_t bytes);
+size_t mi_workspace_bytes(void);
+/* Workspace an entry point needs for the given shape (bytes). */
+size_t mi_layernorm_backward_workspace(int rows, int cols);
+size_t mi_bias_backward_workspace(int rows, int cols);
+size_t mi_embedding_backward_workspace(int batch_seq);
+
+/* ----- LayerNorm --------------------------------------------------------- */
+
+/* y = (x - mean) * inv_std * gamma + beta per row, biased variance,
+ * inv_std = 1/sqrt(var + eps).  Replaces layernorm_forward (kernels.h:53-54,
+ * FINAL_CLEAN_CODE/src/kernels/layernorm.cu:60-66). */
+int mi_layernorm_forward(const float* x, const float* gamma, const float* beta,
+                         float* out, int rows, int cols, float eps, void* stream);
+
+/* As mi_layernorm_forward and also writes mean[rows], inv_std[rows].
+ * Replaces layernorm_forward_save (kernels.h:56-58, layernorm.cu:111-119). */
+int mi_layernorm_forward_save(const float* x, const float* gamma, const float* beta,
+                              float* out, float* mean, float* inv_std,
+                              int rows, int cols, float eps, void* stream);
+
+/* residual_out = a + b; out = LN(residual_out) with saved stats.  Replaces
+ * residual_layernorm_forward_save (kernels.h:60-64, layernorm.cu:173-183). */
+int mi_residual_layernorm_forward_save(const float* a, const float* b,
+                                       const float* gamma, const float* beta,
+                                       float* residual_out, float* out,
+                                       float* mean, float* inv_std,
+                                       int rows, int cols, float eps, void* stream);
+
+/* grad_x = dx (overwrite); dgamma += sum_r g*xhat; dbeta += sum_r g.
+ * Replaces layernorm_backward (kernels.h:66-70, layernorm.cu:273-289). */
+int mi_layernorm_backward(const float* grad_out, const float* x,
+                          const float* mean, const float* inv_std, const float* gamma,
+                          float* grad_x, float* dgamma, float* dbeta,
+                          int rows, int cols, void* stream);
+
+/* grad_residual += dx; dgamma, dbeta accumulate.  Replaces
+ * layernorm_backward_residual (kernels.h:72-76, layernorm.cu:291-308). */
+int mi_layernorm_backward_residual(const float* grad_out, const float* x,
+                                   const float* mean, const float* inv_std,
+                                   const float* gamma, float* grad_residual,
+                                   float* dgamma, float* dbeta,
+                                   int rows, int cols, void* stream);
+
+/* ----- residual / bias / ReLU ------------------------------------------- */
+
+/* out = a + b over n elements; out may alias a or b.  Replaces residual_add
+ * (kernels.h:88, FINAL_CLEAN_CODE/src/kernels/activations.cu:70-82). */
+int mi_residual_add(const float* a, const float* b, float* out, long long n, void* stream);
+
+/* out = (residual + x) + bias[c].  Replaces residual_add_with_bias
+ * (kernels.h:90-92, activations.cu:119-137). */
+int mi_residual_add_with_bias(const float* residual, const float* x, const float* bias,
+                              float* out, int rows, int cols, void* stream);
+
+/* out[r, c] += bias[c] in place.  Replaces bias_add (kernels.h:104,
+ * activations.cu:146-151). */
+int mi_bias_add(float* out, const float* bias, int rows, int cols, void* stream);
+
+/* out = max(in, 0).  Replaces relu_forward (kernels.h:78,
+ * activations.cu:10-14). */
+int mi_relu_forward(const float* in, float* out, long long n, void* stream);
+
+/* grad_in = in > 0 ? grad_out : 0.  Replaces relu_backward (kernels.h:79,
+ * activations.cu:38-50). */
+int mi_relu_backward(const float* in, const float* grad_out, float* grad_in,
+                     long long n, void* stream);
+
+/* out = max(in + bias[c], 0).  Replaces bias_relu_forward (kernels.h:106-107,
+ * activations.cu:181-197). */
+int mi_bias_relu_forward(const float* in, const float* bias, float* out,
+                         int rows, int cols, void* stream);
+
+/* grad_in = mask > 0 ? grad_out : 0; dbias += column sums of grad_in
+ * (deterministic).  Replaces relu_backward_with_bias_backward
+ * (kernels.h:81-83, activations.cu:274-283). */
+int mi_relu_backward_with_bias_backward(const float* mask, const float* grad_out,
+                                        float* grad_in, float* dbias,
+                                        int rows, int cols, void* stream);
+
+/* dbias += column sums of grad (deterministic).  Replaces bias_backward
+ * (kernels.h:111, activations.cu:234-240). */
+int mi_bias_backward(const float* grad, float* dbias, int rows, int cols, void* stream);
+
+/* ----- bias + tanh-GELU (new operators in the slots of bias_relu_forward
+ * and relu_backward_with_bias_backward; the reference has no GELU) ------- */
+
+/* out = gelu_tanh(in + bias[c]). */
+int mi_bias_gelu_forward(const float* in, const float* bias, float* out,
+                         int rows, int cols, void* stream);
+
+/* u = in + bias[c] (recomputed); grad_in = grad_out * gelu_tanh'(u);
+ * dbias += column sums of grad_in (deterministic). */
+int mi_gelu_backward_with_bias_backward(const float* in, const float* bias,
+                                        const float* grad_out, float* grad_in,
+                                        float* dbias, int rows, int cols, void* stream);
+
+/* ----- embedding --------------------------------------------------------- */
+
+/* out[i, :] = table[tokens[i], :].  vocab > 0 bounds the ids: an id outside
+ * [0, vocab) yields a zero row instead of a read out of bounds; vocab <= 0
+ * trusts the ids as the reference does.  Replaces embedding_forward
+ * (kernels.h:131-132, FINAL_CLEAN_CODE/src/kernels/embedding.cu:13-20). */
+int mi_embedding_forward(const float* table, const int* tokens, float* out,
+                         int batch_seq, int dim, int vocab, void* stream);
+
+/* grad_table[tokens[i], :] += grad_out[i, :], each table row accumulated in
+ * increasing i (deterministic, same order as the CPU loop).  vocab > 0
+ * skips ids outside [0, vocab) and sorts only the bits vocab needs; vocab
+ * <= 0 trusts the ids.  Replaces embedding_backward (kernels.h:133-134,
+ * embedding.cu:33-40). */
+int mi_embedding_backward(const float* grad_out, const int* tokens, float* grad_table,
+                          int batch_seq, int dim, int vocab, void* stream);
+
+/* embeddings[b, t, :] += pos_table[t, :] in place.  Replaces
+ * pos_embedding_forward (kernels.h:135-136, embedding.cu:52-59). */
+int mi_pos_embedding_forward(const float* pos_table, float* embeddings,
+                             int batch, int seq, int dim, void* stream);
+
+/* grad_pos[t, :] += sum over b (in increasing b) of grad_out[b, t, :].
+ * Replaces pos_embedding_backward (kernels.h:137-138, embedding.cu:72-79). */
+int mi_pos_embedding_backward(const float* grad_out, float* grad_pos_table,
+                              int batch, int seq, int dim, void* stream);
+
+/* Fused token + position gather: out[b, t, :] = table[id, :] + pos[t, :].
+ * Bit-identical to mi_embedding_forward followed by mi_pos_embedding_forward
+ * (one fp32 add per element), in one pass.  The reference issues the two
+ * calls back to back (FINAL_CLEAN_CODE/src/model/transformer.cu:345-346). */
+int mi_embedding_pos_forward(const float* table, const float* pos_table,
+                             const int* tokens, float* out,
+                             int batch, int seq, int dim, int vocab, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI_KERNELS_H */

@@ -1,0 +1,447 @@
+/*
+ * CPU oracle for the fused non-GEMM layer path (LayerNorm, residual adds,
+ * bias + ReLU / tanh-GELU, token + position embedding).
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker, never the product:
+ * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+ * load liboracle.so.  The HIP library never links or calls it.
+ *
+ * Every float routine restates the reference's host/CPU code statement for
+ * statement (same float type, same sequential summation order, same
+ * evaluation order of each expression).  Where the reference has no CPU
+ * twin, the routine follows the reference GPU kernel's arithmetic with the
+ * reductions done sequentially (cited per function).  Paths below are
+ * relative to the reference root:
+ *   FC/ = FINAL_CLEAN_CODE/, NC/ = NEW_code/.
+ *
+ * Double-precision variants (suffix _f64) give the error budget the tests
+ * log next to the float comparison.
+ *
+ * Built with gcc -O2 -ffp-contract=off (no FMA contraction, SSE2 float
+ * arithmetic), so each expression rounds exactly as written.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static int g_threads = 1;
+
+/* Number of host threads the row-parallel loops use (1 = the reference's
+ * single-threaded CPU path).  Results do not depend on it: rows are
+ * independent and every column sum stays sequential over rows. */
+void orc_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
+int orc_get_threads(void) { return g_threads; }
+
+/* ------------------------------------------------------------------ */
+/* Test-input generators used by the reference's own tests.            */
+/* ------------------------------------------------------------------ */
+
+/* srand(seed) as in FC/tests/test_layernorm.cu:35 and
+ * NC/tests/test_embedding.cu:57. */
+void orc_srand(unsigned seed) { srand(seed); }
+
+/* v = (float)rand()/RAND_MAX - 0.5f, FC/tests/test_layernorm.cu:36 and
+ * NC/tests/test_embedding.cu:58,107,149. Continues the current sequence. */
+void orc_fill_rand_unit(float* v, long n) {
+    for (long i = 0; i < n; ++i) v[i] = (float)rand() / RAND_MAX - 0.5f;
+}
+
+/* t = rand() % vocab, NC/tests/test_embedding.cu:59. */
+void orc_fill_rand_tokens(int* t, long n, int vocab) {
+    for (long i = 0; i < n; ++i) t[i] = rand() % vocab;
+}
+
+/* fill_pattern, FC/tests/test_fusion_benchmark.cu:8-12. */
+void orc_fill_pattern(float* v, long n, float scale, float shift) {
+    for (long i = 0; i < n; ++i)
+        v[i] = scale * sinf(0.013f * (float)i) +
+               0.5f * scale * cosf(0.021f * (float)(i + 7)) + shift;
+}
+
+/* ------------------------------------------------------------------ */
+/* LayerNorm                                                           */
+/* ------------------------------------------------------------------ */
+
+/* LN forward, FC/tests/test_layernorm.cu:8-24 (layernorm_cpu): sequential
+ * float sums, biased variance, inv_std = 1.0f / sqrtf(var + eps).  When
+ * mean / inv_std are non-NULL the row statistics are also saved, as
+ * layernorm_save_kernel does (FC/src/kernels/layernorm.cu:102-105). */
+void orc_layernorm_forward(const float* x, const float* gamma, const float* beta,
+                           float* out, float* save_mean, float* save_inv_std,
+                           int rows, int cols, float eps) {
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
+    for (int r = 0; r < rows; ++r) {
+        const float* xr = x + (long)r * cols;
+        float* yr = out + (long)r * cols;
+        float mean = 0.0f;
+        for (int c = 0; c < cols; ++c) mean += xr[c];
+        mean /= cols;
+        float var = 0.0f;
+        for (int c = 0; c < cols; ++c) {
+            float d = xr[c] - mean;
+            var += d * d;
+        }
+        var /= cols;
+        float inv_std = 1.0f / sqrtf(var + eps);
+        for (int c = 0; c < cols; ++c)
+            yr[c] = (xr[c] - mean) * inv_std * gamma[c] + beta[c];
+        if (save_mean) save_mean[r] = mean;
+        if (save_inv_std) save_inv_std[r] = inv_std;
+    }
+}
+
+/* Double LN forward, FC/tests/test_model_reference.cu:49-68. Inputs are
+ * the float tensors widened to double. */
+void orc_layernorm_forward_f64(const float* x, const float* gamma, const float* beta,
+                               double* out, double* save_mean, double* save_inv_std,
+                               int rows, int cols, double eps) {
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
+    for (int r = 0; r < rows; ++r) {
+        const float* xr = x + (long)r * cols;
+        double mean = 0.0;
+        for (int c = 0; c < cols; ++c) mean += xr[c];
+        mean /= cols;
+        double var = 0.0;
+        for (int c = 0; c < cols; ++c) {
+            double d = xr[c] - mean;
+            var += d * d;
+        }
+        double inv_std = 1.0 / sqrt(var / cols + eps);
+        for (int c = 0; c < cols; ++c)
+            out[(long)r * cols + c] = (xr[c] - mean) * inv_std * gamma[c] + beta[c];
+        if (save_mean) save_mean[r] = mean;
+        if (save_inv_std) save_inv_std[r] = inv_std;
+    }
+}
+
+/* Residual + LN forward: r = a + b (written), then LN(r) with saved stats.
+ * Semantics of residual_layernorm_save_kernel
+ * (FC/src/kernels/layernorm.cu:121-171); FC/tests/test_fusion_benchmark.cu
+ * :162-165 pins it as residual_add followed by layernorm_forward_save. */
+void orc_residual_layernorm_forward(const float* a, const float* b,
+                                    const float* gamma, const float* beta,
+                                    float* residual_out, float* out,
+                                    float* save_mean, float* save_inv_std,
+                                    int rows, int cols, float eps) {
+    long n = (long)rows * cols;
+    for (long i = 0; i < n; ++i) residual_out[i] = a[i] + b[i];
+    orc_layernorm_forward(residual_out, gamma, beta, out, save_mean, save_inv_std,
+                          rows, cols, eps);
+}
+
+/* LN backward.  The reference has no CPU LN backward; this follows the
+ * arithmetic of layernorm_backward_dx_kernel (FC/src/kernels/layernorm.cu
+ * :207-234) with the two row sums done sequentially in float, and of
+ * layernorm_backward_dweight_kernel (:253-267) with each column summed
+ * sequentially over rows and then added into dgamma / dbeta.
+ * add_to_grad = 0: grad_x = dx (layernorm_backward, :273-289);
+ * add_to_grad = 1: grad_x += dx (layernorm_backward_residual, :291-308).
+ * dgamma and dbeta always accumulate (+=), as in the reference. */
+void orc_layernorm_backward(const float* grad_out, const float* x,
+                            const float* mean, const float* inv_std,
+                            const float* gamma, float* grad_x,
+                            float* dgamma, float* dbeta,
+                            int rows, int cols, int add_to_grad) {
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
+    for (int r = 0; r < rows; ++r) {
+        const float* go = grad_out + (long)r * cols;
+        const float* xi = x + (long)r * cols;
+        float* gx = grad_x + (long)r * cols;
+        float mu = mean[r];
+        float is = inv_std[r];
+        float sum_dxhat = 0.0f;
+        float sum_dxhat_xhat = 0.0f;
+        for (int i = 0; i < cols; ++i) {
+            float x_hat = (xi[i] - mu) * is;
+            float dx_hat = go[i] * gamma[i];
+            sum_dxhat += dx_hat;
+            sum_dxhat_xhat += dx_hat * x_hat;
+        }
+        float mean_dxhat = sum_dxhat / cols;
+        float mean_dxhat_xhat = sum_dxhat_xhat / cols;
+        for (int i = 0; i < cols; ++i) {
+            float x_hat = (xi[i] - mu) * is;
+            float dx_hat = go[i] * gamma[i];
+            float dx = is * (dx_hat - mean_dxhat - x_hat * mean_dxhat_xhat);
+            if (add_to_grad)
+                gx[i] += dx;
+            else
+                gx[i] = dx;
+        }
+    }
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
+    for (int c = 0; c < cols; ++c) {
+        float dg = 0.0f;
+        float db = 0.0f;
+        for (int r = 0; r < rows; ++r) {
+            float go = grad_out[(long)r * cols + c];
+            float x_hat = (x[(long)r * cols + c] - mean[r]) * inv_std[r];
+            dg += go * x_hat;
+            db += go;
+        }
+        dgamma[c] += dg;
+        dbeta[c] += db;
+    }
+}
+
+/* Double LN backward from first principles: statistics recomputed in double
+ * from x (as orc_layernorm_forward_f64), dx by the same closed form,
+ * column sums in double.  Outputs are overwritten (no accumulation). */
+void orc_layernorm_backward_f64(const float* grad_out, const float* x,
+                                const float* gamma, double eps,
+                                double* grad_x, double* dgamma, double* dbeta,
+                                int rows, int cols) {
+    double* mu = (double*)malloc(sizeof(double) * (rows > 0 ? rows : 1));
+    double* rs = (double*)malloc(sizeof(double) * (rows > 0 ? rows : 1));
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
+    for (int r = 0; r < rows; ++r) {
+        const float* xi = x + (long)r * cols;
+        const float* go = grad_out + (long)r * cols;
+        double m = 0.0;
+        for (int c = 0; c < cols; ++c) m += xi[c];
+        m /= cols;
+        double v = 0.0;
+        for (int c = 0; c < cols; ++c) {
+            double d = xi[c] - m;
+            v += d * d;
+        }
+        double is = 1.0 / sqrt(v / cols + eps);
+        mu[r] = m;
+        rs[r] = is;
+        double s1 = 0.0, s2 = 0.0;
+        for (int c = 0; c < cols; ++c) {
+            double xh = (xi[c] - m) * is;
+            double dh = (double)go[c] * gamma[c];
+            s1 += dh;
+            s2 += dh * xh;
+        }
+        s1 /= cols;
+        s2 /= cols;
+        for (int c = 0; c < cols; ++c) {
+            double xh = (xi[c] - m) * is;
+            double dh = (double)go[c] * gamma[c];
+            grad_x[(long)r * cols + c] = is * (dh - s1 - xh * s2);
+        }
+    }
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
+    for (int c = 0; c < cols; ++c) {
+        double dg = 0.0, db = 0.0;
+        for (int r = 0; r < rows; ++r) {
+            double go = grad_out[(long)r * cols + c];
+            double xh = (x[(long)r * cols + c] - mu[r]) * rs[r];
+            dg += go * xh;
+            db += go;
+        }
+        dgamma[c] = dg;
+        dbeta[c] = db;
+    }
+    free(mu);
+    free(rs);
+}
+
+/* ------------------------------------------------------------------ */
+/* Residual / bias / ReLU                                              */
+/* ------------------------------------------------------------------ */
+
+/* out = a + b, FC/src/kernels/activations.cu:52-56 (one IEEE add).
+ * In-place (out == a) is allowed, as test_fusion_benchmark.cu:234 uses. */
+void orc_residual_add(const float* a, const float* b, float* out, long n) {
+    for (long i = 0; i < n; ++i) out[i] = a[i] + b[i];
+}
+
+/* out = (residual + x) + bias[c], order of FC/src/kernels/activations.cu
+ * :99-102 and :116 (double form: test_model_reference.cu:175-180). */
+void orc_residual_add_with_bias(const float* residual, const float* x,
+                                const float* bias, float* out, int rows, int cols) {
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c) {
+            long i = (long)r * cols + c;
+            out[i] = residual[i] + x[i] + bias[c];
+        }
+}
+
+/* out += bias[c] in place, FC/src/kernels/activations.cu:139-144. */
+void orc_bias_add(float* out, const float* bias, int rows, int cols) {
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c) out[(long)r * cols + c] += bias[c];
+}
+
+/* FC/src/kernels/activations.cu:5-8. */
+void orc_relu_forward(const float* in, float* out, long n) {
+    for (long i = 0; i < n; ++i) out[i] = (in[i] > 0.0f) ? in[i] : 0.0f;
+}
+
+/* FC/src/kernels/activations.cu:16-20. */
+void orc_relu_backward(const float* in, const float* grad_out, float* grad_in, long n) {
+    for (long i = 0; i < n; ++i) grad_in[i] = (in[i] > 0.0f) ? grad_out[i] : 0.0f;
+}
+
+/* v = in + bias[c]; out = v > 0 ? v : 0, FC/src/kernels/activations.cu
+ * :153-161 (CPU twin in double: test_model_reference.cu:167-172). */
+void orc_bias_relu_forward(const float* in, const float* bias, float* out,
+                           int rows, int cols) {
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c) {
+            long i = (long)r * cols + c;
+            float v = in[i] + bias[c];
+            out[i] = (v > 0.0f) ? v : 0.0f;
+        }
+}
+
+/* dbias[c] += sum_r grad[r, c], sequential over rows.  Semantics of
+ * bias_backward_kernel (FC/src/kernels/activations.cu:221-232), which the
+ * reference sums with float atomics in an unspecified order. */
+void orc_bias_backward(const float* grad, float* dbias, int rows, int cols) {
+    for (int c = 0; c < cols; ++c) {
+        float s = 0.0f;
+        for (int r = 0; r < rows; ++r) s += grad[(long)r * cols + c];
+        dbias[c] += s;
+    }
+}
+
+/* gin = mask > 0 ? g : 0 (written); dbias[c] += sum_r gin.  Semantics of
+ * fused_relu_backward_bias_backward_kernel (FC/src/kernels/activations.cu
+ * :247-272), column sums sequential over rows. */
+void orc_relu_backward_with_bias_backward(const float* mask, const float* grad_out,
+                                          float* grad_in, float* dbias,
+                                          int rows, int cols) {
+    for (int c = 0; c < cols; ++c) {
+        float s = 0.0f;
+        for (int r = 0; r < rows; ++r) {
+            long i = (long)r * cols + c;
+            float g = (mask[i] > 0.0f) ? grad_out[i] : 0.0f;
+            grad_in[i] = g;
+            s += g;
+        }
+        dbias[c] += s;
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* bias + tanh-approximation GELU (no reference twin: the reference uses
+ * bias + ReLU, FC/src/kernels/activations.cu:181-197 / :274-283, and this
+ * pair takes those slots).  Formula: Hendrycks & Gimpel 2016,
+ *   gelu(u) = 0.5 u (1 + tanh(sqrt(2/pi) (u + 0.044715 u^3))),
+ *   gelu'(u) = 0.5 (1 + t) + 0.5 u (1 - t^2) sqrt(2/pi) (1 + 3*0.044715 u^2),
+ * t = tanh(...).  u = in + bias[c] is recomputed in the backward.        */
+/* ------------------------------------------------------------------ */
+
+#define GELU_K0 0.7978845608028654f /* sqrt(2/pi) */
+#define GELU_K1 0.044715f
+
+void orc_bias_gelu_forward(const float* in, const float* bias, float* out,
+                           int rows, int cols) {
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c) {
+            long i = (long)r * cols + c;
+            float u = in[i] + bias[c];
+            float z = GELU_K0 * (u + GELU_K1 * u * u * u);
+            out[i] = 0.5f * u * (1.0f + tanhf(z));
+        }
+}
+
+/* gin = g * gelu'(u) (written); dbias[c] += sum_r gin, sequential over rows. */
+void orc_gelu_backward_with_bias_backward(const float* in, const float* bias,
+                                          const float* grad_out, float* grad_in,
+                                          float* dbias, int rows, int cols) {
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c) {
+            long i = (long)r * cols + c;
+            float u = in[i] + bias[c];
+            float z = GELU_K0 * (u + GELU_K1 * u * u * u);
+            float t = tanhf(z);
+            float d = 0.5f * (1.0f + t) +
+                      0.5f * u * (1.0f - t * t) * GELU_K0 * (1.0f + 3.0f * GELU_K1 * u * u);
+            grad_in[i] = grad_out[i] * d;
+        }
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
+    for (int c = 0; c < cols; ++c) {
+        float s = 0.0f;
+        for (int r = 0; r < rows; ++r) s += grad_in[(long)r * cols + c];
+        dbias[c] += s;
+    }
+}
+
+void orc_bias_gelu_forward_f64(const float* in, const float* bias, double* out,
+                               int rows, int cols) {
+    const double k0 = 0.79788456080286535587989211986876; /* sqrt(2/pi) */
+    const double k1 = 0.044715;
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c) {
+            long i = (long)r * cols + c;
+            double u = (double)in[i] + (double)bias[c];
+            out[i] = 0.5 * u * (1.0 + tanh(k0 * (u + k1 * u * u * u)));
+        }
+}
+
+/* Double backward; u is the float sum in + bias (the value the float paths
+ * see), widened.  dbias is overwritten with the double column sum. */
+void orc_gelu_backward_with_bias_backward_f64(const float* in, const float* bias,
+                                              const float* grad_out, double* grad_in,
+                                              double* dbias, int rows, int cols) {
+    const double k0 = 0.79788456080286535587989211986876;
+    const double k1 = 0.044715;
+    for (int c = 0; c < cols; ++c) dbias[c] = 0.0;
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c) {
+            long i = (long)r * cols + c;
+            double u = (double)(in[i] + bias[c]);
+            double t = tanh(k0 * (u + k1 * u * u * u));
+            double d = 0.5 * (1.0 + t) + 0.5 * u * (1.0 - t * t) * k0 * (1.0 + 3.0 * k1 * u * u);
+            double gi = (double)grad_out[i] * d;
+            grad_in[i] = gi;
+            dbias[c] += gi;
+        }
+}
+
+/* ------------------------------------------------------------------ */
+/* Embedding                                                           */
+/* ------------------------------------------------------------------ */
+
+/* out[i, :] = table[tokens[i], :], NC/tests/test_embedding.cu:16-21. */
+void orc_embedding_forward(const float* table, const int* tokens, float* out,
+                           int batch_seq, int dim) {
+    for (int i = 0; i < batch_seq; ++i)
+        for (int j = 0; j < dim; ++j)
+            out[(long)i * dim + j] = table[(long)tokens[i] * dim + j];
+}
+
+/* grad_table[tokens[i], :] += grad_out[i, :] in increasing i,
+ * NC/tests/test_embedding.cu:23-32.  The reference CPU routine zero-fills
+ * the table first (:26); here the caller zeroes, matching the += contract
+ * of the reference kernel (FC/src/kernels/embedding.cu:22-31). */
+void orc_embedding_backward(const float* grad_out, const int* tokens,
+                            float* grad_table, int batch_seq, int dim) {
+    for (int i = 0; i < batch_seq; ++i) {
+        int tok = tokens[i];
+        for (int j = 0; j < dim; ++j)
+            grad_table[(long)tok * dim + j] += grad_out[(long)i * dim + j];
+    }
+}
+
+/* embeddings[b, s, :] += pos_table[s, :], NC/tests/test_embedding.cu:34-41. */
+void orc_pos_embedding_forward(const float* pos_table, float* embeddings,
+                               int batch, int seq, int dim) {
+    for (int b = 0; b < batch; ++b)
+        for (int s = 0; s < seq; ++s)
+            for (int d = 0; d < dim; ++d)
+                embeddings[((long)b * seq + s) * dim + d] += pos_table[(long)s * dim + d];
+}
+
+/* grad_pos[s, :] += grad_out[b, s, :] for b = 0..batch-1 in order.  No CPU
+ * twin in the reference; semantics of pos_embedding_backward_kernel
+ * (FC/src/kernels/embedding.cu:61-70) with the batch loop sequential. */
+void orc_pos_embedding_backward(const float* grad_out, float* grad_pos_table,
+                                int batch, int seq, int dim) {
+    for (int b = 0; b < batch; ++b)
+        for (int s = 0; s < seq; ++s)
+            for (int d = 0; d < dim; ++d)
+                grad_pos_table[(long)s * dim + d] += grad_out[((long)b * seq + s) * dim + d];
+}

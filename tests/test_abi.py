@@ -1,0 +1,71 @@
+"""CPU checks of the C ABI library: it loads without a GPU, exports every
+symbol include/*.h declares, and rejects bad arguments on the host before
+touching the device."""
+import ctypes
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+import cme213_amd as M
+
+
+def test_library_loads_and_reports_version():
+    assert M.lib.mi_version().decode().startswith("cme213_amd")
+
+
+def test_every_declared_c_symbol_is_exported():
+    names = M.declared_c_symbols()
+    assert len(names) >= 30
+    missing = [n for n in names if not hasattr(M.lib, n)]
+    assert not missing, missing
+    # and the ctypes signature table covers them all
+    assert set(names) <= set(M._SIGS), set(names) - set(M._SIGS)
+
+
+@pytest.mark.skipif(shutil.which("nm") is None, reason="nm not available")
+def test_every_cxx_dropin_symbol_is_exported():
+    with open(M.HEADERS[1]) as f:
+        text = f.read()
+    declared = set(re.findall(r"^void\s+([a-z_0-9]+)\s*\(", text, re.M))
+    assert {"layernorm_forward", "layernorm_backward_residual", "embedding_backward",
+            "bias_gelu_forward", "gelu_backward_with_bias_backward"} <= declared
+    out = subprocess.run(["nm", "-DC", "--defined-only", M.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r" T ([a-z_0-9]+)\(", out))
+    assert declared <= exported, declared - exported
+
+
+def test_host_side_argument_errors():
+    lib = M.lib
+    # invalid shapes are rejected before any HIP call
+    assert lib.mi_layernorm_forward(None, None, None, None, -1, 768, 1e-5, None) == M.MI_ERR_INVALID_ARG
+    assert "invalid shape" in M.last_error()
+    assert lib.mi_layernorm_forward(None, None, None, None, 4, 0, 1e-5, None) == M.MI_ERR_INVALID_ARG
+    assert lib.mi_layernorm_backward(None, None, None, None, None, None, None, None, 8, -3,
+                                     None) == M.MI_ERR_INVALID_ARG
+    assert lib.mi_bias_gelu_forward(None, None, None, -2, 8, None) == M.MI_ERR_INVALID_ARG
+    assert lib.mi_residual_add(None, None, None, -5, None) == M.MI_ERR_INVALID_ARG
+    assert lib.mi_embedding_backward(None, None, None, 16, 0, 0, None) == M.MI_ERR_INVALID_ARG
+    # NULL pointers with a non-empty shape are rejected
+    assert lib.mi_layernorm_forward_save(None, None, None, None, None, None, 4, 8, 1e-5,
+                                         None) == M.MI_ERR_INVALID_ARG
+    assert "NULL" in M.last_error()
+    assert lib.mi_gelu_backward_with_bias_backward(None, None, None, None, None, 4, 8,
+                                                   None) == M.MI_ERR_INVALID_ARG
+    # empty inputs are a successful no-op
+    assert lib.mi_layernorm_forward(None, None, None, None, 0, 768, 1e-5, None) == M.MI_OK
+    assert lib.mi_residual_add(None, None, None, 0, None) == M.MI_OK
+    assert lib.mi_embedding_forward(None, None, None, 0, 768, 0, None) == M.MI_OK
+
+
+def test_workspace_size_queries():
+    ln = M.lib.mi_layernorm_backward_workspace(8192, 768)
+    assert 0 < ln <= 512 * 2 * 768 * 4
+    gb = M.lib.mi_bias_backward_workspace(8192, 3072)
+    assert 0 < gb <= 512 * 3072 * 4
+    eb = M.lib.mi_embedding_backward_workspace(16384)
+    assert eb >= 4 * 16384 * 4
+    assert M.lib.mi_layernorm_backward_workspace(0, 768) == 0

@@ -1,0 +1,394 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+
+Each oracle routine is checked against something independent of its own
+formula:
+  * the reference's own CPU routines, compiled from their source by
+    oracle/build_ref.sh (bit-exact: same float code, same order);
+  * torch's float64 CPU implementations through the committed golden
+    fixtures (tests/golden/, written by make_golden.py);
+  * what the mathematics fixes: central finite differences of the double
+    forward, invariants (sum_c dx = 0, constant rows, odd-part identity of
+    GELU), brute-force float64 sums;
+and a planted-mistake test shows the checks reject a plausible error.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+REF = O.ref()
+needs_ref = pytest.mark.skipif(REF is None, reason="oracle/_ref not built (reference absent)")
+
+
+def rng(seed=0):
+    return np.random.default_rng(seed)
+
+
+# ----------------------------------------------------------------------------
+# Against the reference's own CPU routines (oracle/_ref)
+# ----------------------------------------------------------------------------
+
+@needs_ref
+def test_ln_forward_matches_reference_cpu_srand42():
+    # FC/tests/test_layernorm.cu:29-39: rows=2048, cols=128, srand(42),
+    # x = rand()/RAND_MAX - 0.5, gamma = 1, beta = 0, eps = 1e-5.
+    rows, cols = 2048, 128
+    (x,) = O.rand_unit_sequence(42, [rows * cols])
+    x = x.reshape(rows, cols)
+    gamma = np.ones(cols, np.float32)
+    beta = np.zeros(cols, np.float32)
+    y, m, s = O.layernorm_forward(x, gamma, beta, 1e-5)
+    yr = np.empty_like(x)
+    REF.ref_layernorm_cpu(O._p(x), O._p(gamma), O._p(beta), O._p(yr), rows, cols, 1e-5)
+    assert np.array_equal(y.view(np.uint32), yr.view(np.uint32))
+
+
+@needs_ref
+@pytest.mark.parametrize("rows,cols", [(64, 768), (7, 1600), (5, 33)])
+def test_ln_forward_matches_reference_cpu_random(rows, cols):
+    r = rng(1)
+    x = r.standard_normal((rows, cols)).astype(np.float32)
+    gamma = (1 + 0.02 * r.standard_normal(cols)).astype(np.float32)
+    beta = (0.02 * r.standard_normal(cols)).astype(np.float32)
+    y, _, _ = O.layernorm_forward(x, gamma, beta)
+    yr = np.empty_like(x)
+    REF.ref_layernorm_cpu(O._p(x), O._p(gamma), O._p(beta), O._p(yr), rows, cols, 1e-5)
+    assert np.array_equal(y.view(np.uint32), yr.view(np.uint32))
+
+
+@needs_ref
+def test_ln_forward_f64_matches_reference_double():
+    r = rng(2)
+    rows, cols = 16, 96
+    x = r.standard_normal((rows, cols)).astype(np.float32)
+    gamma = (1 + 0.02 * r.standard_normal(cols)).astype(np.float32)
+    beta = (0.02 * r.standard_normal(cols)).astype(np.float32)
+    y, _, _ = O.layernorm_forward_f64(x, gamma, beta)
+    x64, g64, b64 = (np.ascontiguousarray(a, np.float64) for a in (x, gamma, beta))
+    yr = np.empty_like(x64)
+    REF.ref_layernorm_f64(O._p(x64), O._p(g64), O._p(b64), O._p(yr), rows, cols, 1e-5)
+    assert np.array_equal(y, yr)
+
+
+@needs_ref
+def test_embedding_matches_reference_cpu_srand42():
+    # NC/tests/test_embedding.cu:46-59,103-110,145-155: V=512, D=128, B=16,
+    # T=32; srand(42); table, tokens, grad_out, pos_table drawn in that order.
+    V, D, B, T = 512, 128, 16, 32
+    BT = B * T
+    O.lib().orc_srand(42)
+    table = np.empty(V * D, np.float32)
+    O.lib().orc_fill_rand_unit(O._p(table), table.size)
+    tokens = np.empty(BT, np.int32)
+    O.lib().orc_fill_rand_tokens(O._p(tokens), BT, V)
+    g = np.empty(BT * D, np.float32)
+    O.lib().orc_fill_rand_unit(O._p(g), g.size)
+    pos = np.empty(T * D, np.float32)
+    O.lib().orc_fill_rand_unit(O._p(pos), pos.size)
+    table, g, pos = table.reshape(V, D), g.reshape(BT, D), pos.reshape(T, D)
+
+    out = O.embedding_forward(table, tokens)
+    outr = np.empty_like(out)
+    REF.ref_embedding_forward_cpu(O._p(table), O._p(tokens), O._p(outr), BT, D)
+    assert np.array_equal(out.view(np.uint32), outr.view(np.uint32))
+
+    gt = O.embedding_backward(g, tokens, np.zeros((V, D), np.float32))
+    gtr = np.empty((V, D), np.float32)
+    REF.ref_embedding_backward_cpu(O._p(g), O._p(tokens), O._p(gtr), BT, D, V)
+    assert np.array_equal(gt.view(np.uint32), gtr.view(np.uint32))
+
+    emb = O.pos_embedding_forward(pos, out, B, T)
+    embr = outr.copy()
+    REF.ref_pos_embedding_cpu(O._p(pos), O._p(embr), B, T, D)
+    assert np.array_equal(emb.view(np.uint32), embr.view(np.uint32))
+
+
+@needs_ref
+def test_fill_pattern_matches_reference():
+    for n, scale, shift in [(2048 * 128, 0.1, 0.0), (128, 0.03, 1.0), (512, 0.001, 0.0)]:
+        a = O.fill_pattern(n, scale, shift)
+        b = np.empty(n, np.float32)
+        REF.ref_fill_pattern(O._p(b), n, scale, shift)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+# ----------------------------------------------------------------------------
+# LayerNorm: golden fixtures (torch float64), invariants, finite differences
+# ----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("tag", ["c768", "c33"])
+def test_ln_against_torch_golden(tag):
+    d = np.load(os.path.join(GOLDEN, "layernorm_f64.npz"))
+    x, gamma, beta, g = (d[f"{tag}_{k}"] for k in ("x", "gamma", "beta", "g"))
+    y64, m64, s64 = O.layernorm_forward_f64(x, gamma, beta)
+    np.testing.assert_allclose(y64, d[f"{tag}_y"], rtol=1e-12, atol=1e-12)
+    dx64, dg64, db64 = O.layernorm_backward_f64(g, x, gamma)
+    np.testing.assert_allclose(dx64, d[f"{tag}_dx"], rtol=1e-9, atol=1e-9)
+    np.testing.assert_allclose(dg64, d[f"{tag}_dgamma"], rtol=1e-10, atol=1e-10)
+    np.testing.assert_allclose(db64, d[f"{tag}_dbeta"], rtol=1e-12, atol=1e-12)
+    # float oracle against the same golden values (looser: float rounding)
+    y, m, s = O.layernorm_forward(x, gamma, beta)
+    np.testing.assert_allclose(y, d[f"{tag}_y"], rtol=1e-5, atol=2e-6)
+    dx, dg, db = O.layernorm_backward(g, x, m, s, gamma)
+    np.testing.assert_allclose(dx, d[f"{tag}_dx"], rtol=1e-4, atol=2e-5)
+    np.testing.assert_allclose(dg, d[f"{tag}_dgamma"], rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(db, d[f"{tag}_dbeta"], rtol=1e-5, atol=1e-5)
+
+
+def test_ln_constant_row_gives_beta_exactly():
+    cols = 768
+    x = np.full((3, cols), 0.75, np.float32)
+    gamma = (1 + 0.02 * rng(3).standard_normal(cols)).astype(np.float32)
+    beta = (0.02 * rng(4).standard_normal(cols)).astype(np.float32)
+    y, m, s = O.layernorm_forward(x, gamma, beta)
+    assert np.array_equal(y, np.broadcast_to(beta, y.shape))
+    assert np.all(m == np.float32(0.75))
+    assert np.allclose(s, 1 / np.sqrt(1e-5), rtol=1e-6)
+
+
+def test_ln_unit_affine_moments():
+    r = rng(5)
+    rows, cols = 32, 768
+    x = (3 * r.standard_normal((rows, cols)) + 2).astype(np.float32)
+    y, m, s = O.layernorm_forward(x, np.ones(cols, np.float32), np.zeros(cols, np.float32))
+    y64 = y.astype(np.float64)
+    var = x.astype(np.float64).var(axis=1)
+    assert np.all(np.abs(y64.mean(axis=1)) < 1e-6)
+    np.testing.assert_allclose(y64.var(axis=1), var / (var + 1e-5), rtol=1e-5)
+    np.testing.assert_allclose(m, x.astype(np.float64).mean(axis=1), rtol=1e-5, atol=1e-6)
+
+
+def test_ln_backward_invariants_and_brute_force_columns():
+    r = rng(6)
+    rows, cols = 24, 257
+    x = r.standard_normal((rows, cols)).astype(np.float32)
+    gamma = (1 + 0.1 * r.standard_normal(cols)).astype(np.float32)
+    g = r.standard_normal((rows, cols)).astype(np.float32)
+    dx, dg, db = O.layernorm_backward_f64(g, x, gamma)
+    # sum_c dx = 0 for every row (the mean direction is projected out)
+    assert np.all(np.abs(dx.sum(axis=1)) < 1e-10 * np.abs(dx).sum(axis=1).max())
+    # brute-force column sums in float64
+    x64 = x.astype(np.float64)
+    mu = x64.mean(axis=1, keepdims=True)
+    rs = 1 / np.sqrt(((x64 - mu) ** 2).mean(axis=1, keepdims=True) + 1e-5)
+    xh = (x64 - mu) * rs
+    np.testing.assert_allclose(dg, (g * xh).sum(axis=0), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(db, g.astype(np.float64).sum(axis=0), rtol=1e-12, atol=1e-12)
+
+
+def _ln_f64_np(x, gamma, beta, eps=1e-5):
+    mu = x.mean(axis=1, keepdims=True)
+    var = ((x - mu) ** 2).mean(axis=1, keepdims=True)
+    return (x - mu) / np.sqrt(var + eps) * gamma + beta
+
+
+def test_ln_backward_finite_differences():
+    # d/dx of sum(g * LN(x)) by central differences of the double forward
+    r = rng(7)
+    rows, cols = 3, 40
+    x = r.standard_normal((rows, cols)).astype(np.float32)
+    gamma = (1 + 0.1 * r.standard_normal(cols)).astype(np.float32)
+    beta = (0.1 * r.standard_normal(cols)).astype(np.float32)
+    g = r.standard_normal((rows, cols)).astype(np.float32)
+    dx, dg, db = O.layernorm_backward_f64(g, x, gamma)
+    x64, g64, ga64, be64 = (a.astype(np.float64) for a in (x, g, gamma, beta))
+    h = 1e-6
+    num = np.zeros_like(x64)
+    for i in range(rows):
+        for j in range(cols):
+            xp, xm = x64.copy(), x64.copy()
+            xp[i, j] += h
+            xm[i, j] -= h
+            num[i, j] = ((g64 * _ln_f64_np(xp, ga64, be64)).sum()
+                         - (g64 * _ln_f64_np(xm, ga64, be64)).sum()) / (2 * h)
+    np.testing.assert_allclose(dx, num, rtol=1e-6, atol=1e-7)
+    num_g = np.zeros(cols)
+    for j in range(cols):
+        gp, gm = ga64.copy(), ga64.copy()
+        gp[j] += h
+        gm[j] -= h
+        num_g[j] = ((g64 * _ln_f64_np(x64, gp, be64)).sum()
+                    - (g64 * _ln_f64_np(x64, gm, be64)).sum()) / (2 * h)
+    np.testing.assert_allclose(dg, num_g, rtol=1e-6, atol=1e-7)
+
+
+def test_ln_backward_float_oracle_close_to_f64_and_residual_mode():
+    r = rng(8)
+    rows, cols = 64, 768
+    x = r.standard_normal((rows, cols)).astype(np.float32)
+    gamma = (1 + 0.02 * r.standard_normal(cols)).astype(np.float32)
+    beta = (0.02 * r.standard_normal(cols)).astype(np.float32)
+    g = r.standard_normal((rows, cols)).astype(np.float32)
+    _, m, s = O.layernorm_forward(x, gamma, beta)
+    dx, dg, db = O.layernorm_backward(g, x, m, s, gamma)
+    dx64, dg64, db64 = O.layernorm_backward_f64(g, x, gamma)
+    np.testing.assert_allclose(dx, dx64, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(dg, dg64, rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(db, db64, rtol=1e-4, atol=1e-4)
+    # residual mode adds dx onto grad_residual; dgamma/dbeta accumulate
+    res0 = r.standard_normal((rows, cols)).astype(np.float32)
+    dg0 = r.standard_normal(cols).astype(np.float32)
+    rx, rdg, rdb = O.layernorm_backward(g, x, m, s, gamma, grad_x=res0, dgamma=dg0,
+                                        dbeta=dg0, add_to_grad=True)
+    assert np.array_equal(rx, res0 + dx)
+    assert np.array_equal(rdg, dg0 + dg)
+
+
+def test_residual_layernorm_is_add_then_layernorm():
+    # FC/tests/test_fusion_benchmark.cu:162-165 pins the fused op as
+    # residual_add followed by layernorm_forward_save.
+    n = 2048 * 128
+    a = O.fill_pattern(n, 0.1).reshape(2048, 128)
+    b = O.fill_pattern(n, 0.08).reshape(2048, 128)
+    gamma = O.fill_pattern(128, 0.03, 1.0)
+    beta = O.fill_pattern(128, 0.02)
+    r, y, m, s = O.residual_layernorm_forward(a, b, gamma, beta)
+    assert np.array_equal(r, a + b)
+    y2, m2, s2 = O.layernorm_forward(a + b, gamma, beta)
+    assert np.array_equal(y, y2) and np.array_equal(m, m2) and np.array_equal(s, s2)
+
+
+# ----------------------------------------------------------------------------
+# GELU: golden fixture (torch float64), identities, finite differences
+# ----------------------------------------------------------------------------
+
+def test_gelu_against_torch_golden():
+    d = np.load(os.path.join(GOLDEN, "gelu_tanh_f64.npz"))
+    u, g = d["u"], d["g"]
+    x = u.reshape(1, -1)
+    zero_bias = np.zeros(u.size, np.float32)
+    y64 = O.bias_gelu_forward_f64(x, zero_bias)[0]
+    # Both float64 evaluations of 1 + tanh(z) cancel for u < -10 (true value
+    # < 1e-40); they agree to 1e-15 absolute there.
+    np.testing.assert_allclose(y64, d["y"], rtol=1e-13, atol=1e-15)
+    gin64, _ = O.gelu_backward_with_bias_backward_f64(x, zero_bias, g.reshape(1, -1))
+    np.testing.assert_allclose(gin64[0], d["gin"], rtol=1e-12, atol=1e-14)
+    # float oracle (textbook float formula with tanhf)
+    y = O.bias_gelu_forward(x, zero_bias)[0]
+    np.testing.assert_allclose(y, d["y"], rtol=1e-5, atol=1e-6)
+    gin, _ = O.gelu_backward_with_bias_backward(x, zero_bias, g.reshape(1, -1))
+    np.testing.assert_allclose(gin[0], d["gin"], rtol=1e-4, atol=1e-6)
+
+
+def test_gelu_identities():
+    u = np.linspace(-8, 8, 1601).astype(np.float32)
+    x = u.reshape(1, -1)
+    zb = np.zeros(u.size, np.float32)
+    y = O.bias_gelu_forward_f64(x, zb)[0]
+    ym = O.bias_gelu_forward_f64(-x, zb)[0]
+    # odd part: gelu(u) - gelu(-u) = u (exactly, since tanh is odd)
+    np.testing.assert_allclose(y - ym, u.astype(np.float64), rtol=0, atol=1e-12)
+    assert O.bias_gelu_forward_f64(np.zeros((1, 1), np.float32), np.zeros(1, np.float32))[0, 0] == 0
+    d0, _ = O.gelu_backward_with_bias_backward_f64(np.zeros((1, 1), np.float32),
+                                                   np.zeros(1, np.float32),
+                                                   np.ones((1, 1), np.float32))
+    assert d0[0, 0] == 0.5
+    big = np.array([[30.0, -30.0]], np.float32)
+    yb = O.bias_gelu_forward_f64(big, np.zeros(2, np.float32))[0]
+    assert yb[0] == 30.0 and abs(yb[1]) < 1e-300
+
+
+def test_gelu_backward_finite_differences_and_bias():
+    r = rng(9)
+    rows, cols = 6, 50
+    x = (1.5 * r.standard_normal((rows, cols))).astype(np.float32)
+    b = (0.02 * r.standard_normal(cols)).astype(np.float32)
+    g = r.standard_normal((rows, cols)).astype(np.float32)
+    gin, db = O.gelu_backward_with_bias_backward_f64(x, b, g)
+    u = (x + b).astype(np.float64)
+    h = 1e-6
+    k0 = np.sqrt(2 / np.pi)
+
+    def gelu(v):
+        return 0.5 * v * (1 + np.tanh(k0 * (v + 0.044715 * v ** 3)))
+
+    num = g * (gelu(u + h) - gelu(u - h)) / (2 * h)
+    np.testing.assert_allclose(gin, num, rtol=1e-7, atol=1e-9)
+    np.testing.assert_allclose(db, num.sum(axis=0), rtol=1e-7, atol=1e-9)
+    ginf, dbf = O.gelu_backward_with_bias_backward(x, b, g)
+    np.testing.assert_allclose(ginf, gin, rtol=1e-4, atol=1e-6)
+    np.testing.assert_allclose(dbf, db, rtol=1e-4, atol=1e-5)
+
+
+# ----------------------------------------------------------------------------
+# residual / bias / ReLU / embedding position backward: brute force
+# ----------------------------------------------------------------------------
+
+def test_elementwise_ops_against_numpy():
+    r = rng(10)
+    rows, cols = 37, 96
+    a = r.standard_normal((rows, cols)).astype(np.float32)
+    b = r.standard_normal((rows, cols)).astype(np.float32)
+    bias = r.standard_normal(cols).astype(np.float32)
+    assert np.array_equal(O.residual_add(a, b), a + b)
+    assert np.array_equal(O.residual_add_with_bias(a, b, bias), (a + b) + bias)
+    assert np.array_equal(O.bias_add(a, bias), a + bias)
+    assert np.array_equal(O.relu_forward(a), np.where(a > 0, a, np.float32(0)))
+    assert np.array_equal(O.relu_backward(a, b), np.where(a > 0, b, np.float32(0)))
+    assert np.array_equal(O.bias_relu_forward(a, bias),
+                          np.where(a + bias > 0, a + bias, np.float32(0)))
+    gin, db = O.relu_backward_with_bias_backward(a, b)
+    assert np.array_equal(gin, np.where(a > 0, b, np.float32(0)))
+    np.testing.assert_allclose(db, gin.astype(np.float64).sum(axis=0), rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(O.bias_backward(b), b.astype(np.float64).sum(axis=0), rtol=1e-5,
+                               atol=1e-5)
+
+
+def test_pos_embedding_backward_is_sum_over_batch():
+    r = rng(11)
+    B, T, D = 5, 7, 12
+    g = r.standard_normal((B * T, D)).astype(np.float32)
+    gp0 = r.standard_normal((T, D)).astype(np.float32)
+    gp = O.pos_embedding_backward(g, gp0, B, T)
+    expect = gp0.copy()
+    for bb in range(B):
+        expect = expect + g[bb * T:(bb + 1) * T]
+    assert np.array_equal(gp, expect)
+
+
+def test_embedding_backward_accumulates_in_token_order():
+    r = rng(12)
+    V, D, BT = 9, 16, 40
+    tokens = r.integers(0, V, BT).astype(np.int32)
+    g = r.standard_normal((BT, D)).astype(np.float32)
+    gt0 = r.standard_normal((V, D)).astype(np.float32)
+    gt = O.embedding_backward(g, tokens, gt0)
+    expect = gt0.copy()
+    for i in range(BT):
+        expect[tokens[i]] = expect[tokens[i]] + g[i]
+    assert np.array_equal(gt, expect)
+
+
+# ----------------------------------------------------------------------------
+# The checks above reject a plausible mistake (planted in a CPU copy).
+# ----------------------------------------------------------------------------
+
+def test_planted_mistake_in_ln_backward_is_caught():
+    d = np.load(os.path.join(GOLDEN, "layernorm_f64.npz"))
+    x, gamma, g = d["c768_x"].astype(np.float64), d["c768_gamma"].astype(np.float64), \
+        d["c768_g"].astype(np.float64)
+    mu = x.mean(axis=1, keepdims=True)
+    rs = 1 / np.sqrt(((x - mu) ** 2).mean(axis=1, keepdims=True) + 1e-5)
+    xh = (x - mu) * rs
+    dh = g * gamma
+    # dropped x_hat * mean(dh * x_hat) term
+    wrong = rs * (dh - dh.mean(axis=1, keepdims=True))
+    assert not np.allclose(wrong, d["c768_dx"], rtol=1e-4, atol=1e-5)
+    # wrong sign of the projection term
+    wrong2 = rs * (dh - dh.mean(axis=1, keepdims=True) + xh * (dh * xh).mean(axis=1, keepdims=True))
+    assert not np.allclose(wrong2, d["c768_dx"], rtol=1e-4, atol=1e-5)
+    right = rs * (dh - dh.mean(axis=1, keepdims=True) - xh * (dh * xh).mean(axis=1, keepdims=True))
+    np.testing.assert_allclose(right, d["c768_dx"], rtol=1e-9, atol=1e-9)
+
+
+def test_planted_mistake_in_gelu_derivative_is_caught():
+    d = np.load(os.path.join(GOLDEN, "gelu_tanh_f64.npz"))
+    u = d["u"].astype(np.float64)
+    k0 = np.sqrt(2 / np.pi)
+    t = np.tanh(k0 * (u + 0.044715 * u ** 3))
+    # missing the factor 3 in the cubic term's derivative
+    wrong = 0.5 * (1 + t) + 0.5 * u * (1 - t * t) * k0 * (1 + 0.044715 * u * u)
+    assert not np.allclose(d["g"] * wrong, d["gin"], rtol=1e-4, atol=1e-6)

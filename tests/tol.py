@@ -1,0 +1,60 @@
+"""Tolerances of the parity tests (stated once, used everywhere).
+
+Forward fp32 outputs (LayerNorm y, GELU y):      |gpu - ref| <= 1e-6 + 1e-5 |ref|
+Element-wise backward outputs (dx, grad_in):     |gpu - ref| <= 1e-6 s + 1e-4 |ref|,
+                                                 s = max(1, rms(ref))
+Column sums (dgamma, dbeta, dbias):              |gpu - ref| <= 1e-4 (|ref| + ||t_c||_2)
+    where t_c are the per-row terms summed into column c; the float error of
+    any summation order scales with ||t_c||_2, so a column whose sum cancels
+    to near zero is still held to 1e-4 of its natural size.
+Gather / copies / single adds / selects:         bit-exact.
+"""
+import numpy as np
+
+FWD_RTOL, FWD_ATOL = 1e-5, 1e-6
+BWD_RTOL, BWD_ATOL = 1e-4, 1e-6
+COL_RTOL = 1e-4
+
+
+def _report(name, gpu, ref, bound):
+    err = np.abs(gpu.astype(np.float64) - ref.astype(np.float64))
+    bad = err > bound
+    if bad.any():
+        i = np.unravel_index(np.argmax(err - bound), err.shape)
+        raise AssertionError(
+            f"{name}: {int(bad.sum())} of {err.size} elements out of tolerance; worst at {i}: "
+            f"gpu={gpu[i]!r} ref={ref[i]!r} err={err[i]:.3e} bound={bound[i] if np.ndim(bound) else bound:.3e}")
+    return float(err.max()) if err.size else 0.0
+
+
+def assert_fwd(name, gpu, ref):
+    ref = np.asarray(ref)
+    bound = FWD_ATOL + FWD_RTOL * np.abs(ref.astype(np.float64))
+    return _report(name, np.asarray(gpu), ref, bound)
+
+
+def assert_bwd(name, gpu, ref):
+    ref = np.asarray(ref)
+    r64 = ref.astype(np.float64)
+    s = max(1.0, float(np.sqrt(np.mean(r64 * r64)))) if r64.size else 1.0
+    bound = BWD_ATOL * s + BWD_RTOL * np.abs(r64)
+    return _report(name, np.asarray(gpu), ref, bound)
+
+
+def assert_colsum(name, gpu, ref, terms):
+    """terms: [rows, cols] array of the per-row summands (float64 ok)."""
+    ref = np.asarray(ref)
+    t = np.asarray(terms, dtype=np.float64)
+    l2 = np.sqrt((t * t).sum(axis=0))
+    bound = COL_RTOL * (np.abs(ref.astype(np.float64)) + l2)
+    return _report(name, np.asarray(gpu), ref, bound)
+
+
+def assert_exact(name, gpu, ref):
+    gpu, ref = np.asarray(gpu), np.asarray(ref)
+    assert gpu.shape == ref.shape, f"{name}: shape {gpu.shape} vs {ref.shape}"
+    same = (gpu.view(np.uint32) == ref.view(np.uint32)) if gpu.dtype == np.float32 else (gpu == ref)
+    if not same.all():
+        i = np.unravel_index(np.argmin(same), same.shape)
+        raise AssertionError(f"{name}: {int((~same).sum())} elements differ bitwise; first at "
+                             f"{i}: gpu={gpu[i]!r} ref={ref[i]!r}")
