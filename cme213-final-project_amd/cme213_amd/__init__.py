@@ -43,6 +43,16 @@ if not os.path.exists(LIB_PATH):
         f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "
         "(the HIP library is required; there is no CPU fallback)")
 
+# torch wheels bundle their own libamdhip64 / libhsa-runtime64 (same sonames
+# as /opt/rocm's).  Loading torch first makes this library bind to the runtime
+# torch already holds, so one process never initialises two HIP runtimes
+# (which leaves one of them without devices).  Without torch, the system
+# runtime is used.
+try:
+    import torch  # noqa: F401
+except ImportError:
+    pass
+
 lib = ctypes.CDLL(LIB_PATH)
 
 P = c_void_p

@@ -29,7 +29,13 @@ namespace mi {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 4;
+#ifndef MI_EW_UNROLL
+#define MI_EW_UNROLL 4
+#endif
+#ifndef MI_FWD_ROWS_PER_TILE
+#define MI_FWD_ROWS_PER_TILE 8
+#endif
+constexpr int kUnroll = MI_EW_UNROLL;
 
 // ---------------------------------------------------------------------------
 // tanh-approximation GELU (Hendrycks & Gimpel 2016):
@@ -79,11 +85,11 @@ struct AddOp {
     const float* b;
     float* out;
     __device__ void operator()(size_t i) const {
-        const fvec<W> x = vload<W>(a, i), y = vload<W>(b, i);
+        const fvec<W> x = sload<W>(a, i), y = sload<W>(b, i);
         fvec<W> o;
 #pragma unroll
         for (int e = 0; e < W; ++e) o.v[e] = x.v[e] + y.v[e];
-        vstore<W>(out, i, o);
+        sstore<W>(out, i, o);
     }
 };
 
@@ -92,11 +98,11 @@ struct ReluOp {
     const float* in;
     float* out;
     __device__ void operator()(size_t i) const {
-        const fvec<W> x = vload<W>(in, i);
+        const fvec<W> x = sload<W>(in, i);
         fvec<W> o;
 #pragma unroll
         for (int e = 0; e < W; ++e) o.v[e] = (x.v[e] > 0.0f) ? x.v[e] : 0.0f;
-        vstore<W>(out, i, o);
+        sstore<W>(out, i, o);
     }
 };
 
@@ -106,11 +112,11 @@ struct ReluBwdOp {
     const float* g;
     float* gin;
     __device__ void operator()(size_t i) const {
-        const fvec<W> x = vload<W>(in, i), d = vload<W>(g, i);
+        const fvec<W> x = sload<W>(in, i), d = sload<W>(g, i);
         fvec<W> o;
 #pragma unroll
         for (int e = 0; e < W; ++e) o.v[e] = (x.v[e] > 0.0f) ? d.v[e] : 0.0f;
-        vstore<W>(gin, i, o);
+        sstore<W>(gin, i, o);
     }
 };
 
@@ -183,12 +189,12 @@ struct ResidBiasOp {  // out = (a + x) + bias
     struct In {
         fvec<W> a, x;
     };
-    __device__ In load(size_t i) const { return {vload<W>(a, i), vload<W>(x, i)}; }
+    __device__ In load(size_t i) const { return {sload<W>(a, i), sload<W>(x, i)}; }
     __device__ fvec<W> apply(size_t i, const In& in, const fvec<W>& b) const {
         fvec<W> o;
 #pragma unroll
         for (int e = 0; e < W; ++e) o.v[e] = in.a.v[e] + in.x.v[e] + b.v[e];
-        vstore<W>(out, i, o);
+        sstore<W>(out, i, o);
         return o;
     }
 };
@@ -199,12 +205,12 @@ struct BiasAddOp {  // out += bias (in place)
     struct In {
         fvec<W> o;
     };
-    __device__ In load(size_t i) const { return {vload<W>(out, i)}; }
+    __device__ In load(size_t i) const { return {sload<W>(out, i)}; }
     __device__ fvec<W> apply(size_t i, const In& in, const fvec<W>& b) const {
         fvec<W> o;
 #pragma unroll
         for (int e = 0; e < W; ++e) o.v[e] = in.o.v[e] + b.v[e];
-        vstore<W>(out, i, o);
+        sstore<W>(out, i, o);
         return o;
     }
 };
@@ -216,7 +222,7 @@ struct BiasReluOp {  // out = max(in + bias, 0)
     struct In {
         fvec<W> x;
     };
-    __device__ In load(size_t i) const { return {vload<W>(in, i)}; }
+    __device__ In load(size_t i) const { return {sload<W>(in, i)}; }
     __device__ fvec<W> apply(size_t i, const In& v, const fvec<W>& b) const {
         fvec<W> o;
 #pragma unroll
@@ -224,7 +230,7 @@ struct BiasReluOp {  // out = max(in + bias, 0)
             const float t = v.x.v[e] + b.v[e];
             o.v[e] = (t > 0.0f) ? t : 0.0f;
         }
-        vstore<W>(out, i, o);
+        sstore<W>(out, i, o);
         return o;
     }
 };
@@ -236,12 +242,12 @@ struct BiasGeluOp {  // out = gelu(in + bias)
     struct In {
         fvec<W> x;
     };
-    __device__ In load(size_t i) const { return {vload<W>(in, i)}; }
+    __device__ In load(size_t i) const { return {sload<W>(in, i)}; }
     __device__ fvec<W> apply(size_t i, const In& v, const fvec<W>& b) const {
         fvec<W> o;
 #pragma unroll
         for (int e = 0; e < W; ++e) o.v[e] = gelu_fwd(v.x.v[e] + b.v[e]);
-        vstore<W>(out, i, o);
+        sstore<W>(out, i, o);
         return o;
     }
 };
@@ -252,7 +258,7 @@ struct ColSumOp {  // dbias partials of grad
     struct In {
         fvec<W> g;
     };
-    __device__ In load(size_t i) const { return {vload<W>(g, i)}; }
+    __device__ In load(size_t i) const { return {sload<W>(g, i)}; }
     __device__ fvec<W> apply(size_t, const In& v, const fvec<W>&) const { return v.g; }
 };
 
@@ -264,12 +270,12 @@ struct ReluBwdBiasOp {  // gin = mask > 0 ? g : 0
     struct In {
         fvec<W> m, g;
     };
-    __device__ In load(size_t i) const { return {vload<W>(mask, i), vload<W>(g, i)}; }
+    __device__ In load(size_t i) const { return {sload<W>(mask, i), sload<W>(g, i)}; }
     __device__ fvec<W> apply(size_t i, const In& v, const fvec<W>&) const {
         fvec<W> o;
 #pragma unroll
         for (int e = 0; e < W; ++e) o.v[e] = (v.m.v[e] > 0.0f) ? v.g.v[e] : 0.0f;
-        vstore<W>(gin, i, o);
+        sstore<W>(gin, i, o);
         return o;
     }
 };
@@ -282,12 +288,12 @@ struct GeluBwdBiasOp {  // gin = g * gelu'(in + bias)
     struct In {
         fvec<W> x, g;
     };
-    __device__ In load(size_t i) const { return {vload<W>(in, i), vload<W>(g, i)}; }
+    __device__ In load(size_t i) const { return {sload<W>(in, i), sload<W>(g, i)}; }
     __device__ fvec<W> apply(size_t i, const In& v, const fvec<W>& b) const {
         fvec<W> o;
 #pragma unroll
         for (int e = 0; e < W; ++e) o.v[e] = v.g.v[e] * gelu_grad(v.x.v[e] + b.v[e]);
-        vstore<W>(gin, i, o);
+        sstore<W>(gin, i, o);
         return o;
     }
 };
@@ -300,7 +306,7 @@ int check_shape(const char* name, int rows, int cols) {
 }
 
 // Rows per tile for the non-reducing broadcast kernels.
-constexpr int kFwdRowsPerTile = 8;
+constexpr int kFwdRowsPerTile = MI_FWD_ROWS_PER_TILE;
 
 template <int W, class Op>
 int launch_rowtile(const char* name, Op op, const float* bias, int rows, int cols,

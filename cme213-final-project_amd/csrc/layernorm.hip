@@ -53,12 +53,12 @@ __global__ __launch_bounds__(kFwdWaves * kWave) void ln_fwd_wave_kernel(
     for (int k = 0; k < N; ++k) {
         const int j = lane + k * kWave;
         if (j < nv) {
-            v[k] = vload<W>(a + base, j);
+            v[k] = sload<W>(a + base, j);
             if constexpr (RESID) {
-                const fvec<W> w = vload<W>(b + base, j);
+                const fvec<W> w = sload<W>(b + base, j);
 #pragma unroll
                 for (int e = 0; e < W; ++e) v[k].v[e] = v[k].v[e] + w.v[e];
-                vstore<W>(resid_out + base, j, v[k]);
+                sstore<W>(resid_out + base, j, v[k]);
             }
         } else {
             v[k] = vzero<W>();
@@ -100,7 +100,7 @@ __global__ __launch_bounds__(kFwdWaves * kWave) void ln_fwd_wave_kernel(
             fvec<W> y;
 #pragma unroll
             for (int e = 0; e < W; ++e) y.v[e] = (v[k].v[e] - mean) * rstd * g.v[e] + bt.v[e];
-            vstore<W>(out + base, j, y);
+            sstore<W>(out + base, j, y);
         }
     }
 }
@@ -201,8 +201,8 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void ln_bwd_group_kernel(
         for (int k = 0; k < N; ++k) {
             const int j = t + k * GT;
             const bool ok = valid && j < nv;
-            go[k] = ok ? vload<W>(gout + off, j) : vzero<W>();
-            xv[k] = ok ? vload<W>(x + off, j) : vzero<W>();
+            go[k] = ok ? sload<W>(gout + off, j) : vzero<W>();
+            xv[k] = ok ? sload<W>(x + off, j) : vzero<W>();
         }
         const float mu = valid ? mean[row] : 0.0f;
         const float is = valid ? rstd[row] : 0.0f;
@@ -247,7 +247,7 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void ln_bwd_group_kernel(
                 const int j = t + k * GT;
                 if (j < nv) {
                     fvec<W> d;
-                    if constexpr (ADD) d = vload<W>(gx + off, j);
+                    if constexpr (ADD) d = sload<W>(gx + off, j);
 #pragma unroll
                     for (int e = 0; e < W; ++e) {
                         const float xh = (xv[k].v[e] - mu) * is;
@@ -260,7 +260,7 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void ln_bwd_group_kernel(
                         ag[k].v[e] += go[k].v[e] * xh;
                         ab[k].v[e] += go[k].v[e];
                     }
-                    vstore<W>(gx + off, j, d);
+                    sstore<W>(gx + off, j, d);
                 }
             }
         }

@@ -46,6 +46,39 @@ __device__ __forceinline__ void vstore(float* base, size_t vec_index, const fvec
     reinterpret_cast<fvec<W>*>(base)[vec_index] = x;
 }
 
+// Loads / stores of activation tensors that are touched once per call.
+// With MI_STREAM_NT_LOAD / MI_STREAM_NT_STORE set to 1 they carry the
+// non-temporal hint (global_load/store ... nt), which asks the caches not to
+// retain the lines; by default they are ordinary accesses.
+#ifndef MI_STREAM_NT_LOAD
+#define MI_STREAM_NT_LOAD 0
+#endif
+#ifndef MI_STREAM_NT_STORE
+#define MI_STREAM_NT_STORE 0
+#endif
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int W>
+__device__ __forceinline__ fvec<W> sload(const float* base, size_t vec_index) {
+    if constexpr (W == 4 && MI_STREAM_NT_LOAD) {
+        const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(base) + vec_index);
+        return fvec<4>{{t.x, t.y, t.z, t.w}};
+    } else {
+        return vload<W>(base, vec_index);
+    }
+}
+
+template <int W>
+__device__ __forceinline__ void sstore(float* base, size_t vec_index, const fvec<W>& x) {
+    if constexpr (W == 4 && MI_STREAM_NT_STORE) {
+        const f32x4 t = {x.v[0], x.v[1], x.v[2], x.v[3]};
+        __builtin_nontemporal_store(t, reinterpret_cast<f32x4*>(base) + vec_index);
+    } else {
+        vstore<W>(base, vec_index, x);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Wave64 sum.  Four DPP steps reduce each 16-lane row (quad xor-1, quad
 // xor-2, half-row mirror, row mirror); the four row totals are then read

@@ -18,6 +18,7 @@ namespace mi {
 namespace {
 
 constexpr int kFinWaves = 16;
+constexpr int kChunk = 32;
 
 __global__ __launch_bounds__(kFinWaves * kWave) void colsum_finalize_kernel(
     const float* __restrict__ part, int P, int ncols, float* __restrict__ out0, int split,
@@ -28,21 +29,20 @@ __global__ __launch_bounds__(kFinWaves * kWave) void colsum_finalize_kernel(
     const int c = blockIdx.x * kWave + lane;
     const int p0 = static_cast<int>(static_cast<long long>(wave) * P / kFinWaves);
     const int p1 = static_cast<int>(static_cast<long long>(wave + 1) * P / kFinWaves);
+    // All loads of a chunk are issued before the first add, so a wave waits
+    // for one memory round trip per kChunk partial rows.
     float s = 0.0f;
     if (c < ncols) {
         const float* col = part + c;
-        int p = p0;
-        for (; p + 4 <= p1; p += 4) {
-            const float a0 = col[static_cast<size_t>(p) * ncols];
-            const float a1 = col[static_cast<size_t>(p + 1) * ncols];
-            const float a2 = col[static_cast<size_t>(p + 2) * ncols];
-            const float a3 = col[static_cast<size_t>(p + 3) * ncols];
-            s += a0;
-            s += a1;
-            s += a2;
-            s += a3;
+        for (int pb = p0; pb < p1; pb += kChunk) {
+            float v[kChunk];
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k)
+                v[k] = (pb + k < p1) ? col[static_cast<size_t>(pb + k) * ncols] : 0.0f;
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k)
+                if (pb + k < p1) s += v[k];
         }
-        for (; p < p1; ++p) s += col[static_cast<size_t>(p) * ncols];
     }
     tot[wave][lane] = s;
     __syncthreads();

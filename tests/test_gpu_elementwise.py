@@ -8,7 +8,8 @@ import torch
 import cme213_amd as M
 import oracle as O
 from gpu_util import dev_t, gelu_inputs, host, note
-from tol import assert_bwd, assert_colsum, assert_exact, assert_fwd
+from tol import (assert_bwd, assert_bwd_within_oracle_error, assert_colsum, assert_exact,
+                 assert_fwd, assert_fwd_within_oracle_error)
 
 pytestmark = pytest.mark.gpu
 
@@ -75,8 +76,16 @@ def test_bias_and_relu_family(dev, rows, cols):
     (1, 3072, 6),
 ])
 def test_bias_gelu_forward_backward(dev, rows, cols, seed):
+    # GELU has no reference implementation; its reference is the published
+    # formula.  The parity target is the float64 evaluation of that formula
+    # (orc_*_f64, pinned to torch's float64 GELU by the golden fixture), at the
+    # stated fwd / bwd tolerances.  Against the float oracle (the textbook
+    # float formula) the bound is the same tolerance plus that oracle's own
+    # rounding error, which is large where 1 + tanhf(z) cancels (u < -4).
     note(f"gelu rows={rows} cols={cols} seed={seed}")
     x, b, g = gelu_inputs(rows, cols, seed)
+    y64 = O.bias_gelu_forward_f64(x, b)
+    gin64, db64 = O.gelu_backward_with_bias_backward_f64(x, b, g)
     y_o = O.bias_gelu_forward(x, b)
     db0 = np.full(cols, 0.125, np.float32)
     gin_o, db_o = O.gelu_backward_with_bias_backward(x, b, g, dbias=db0)
@@ -85,27 +94,25 @@ def test_bias_gelu_forward_backward(dev, rows, cols, seed):
     Y = torch.empty_like(X)
     M.bias_gelu_forward(X, Bi, Y, rows, cols)
     y = host(Y)
-    assert_fwd("gelu y", y, y_o)
+    assert_fwd("gelu y vs f64", y, y64)
+    assert_fwd_within_oracle_error("gelu y vs float oracle", y, y_o, y64)
     GIN = torch.empty_like(X)
     DB = dev_t(db0)
     M.gelu_backward_with_bias_backward(X, Bi, G, GIN, DB, rows, cols)
     gin = host(GIN)
-    assert_bwd("gelu grad_in", gin, gin_o)
-    assert_colsum("gelu dbias", host(DB), db_o, gin_o)
+    assert_bwd("gelu grad_in vs f64", gin, gin64)
+    assert_bwd_within_oracle_error("gelu grad_in vs float oracle", gin, gin_o, gin64)
+    db = host(DB)
+    assert_colsum("gelu dbias vs f64", db, db64 + db0.astype(np.float64), gin64)
+    assert_colsum("gelu dbias vs float oracle", db, db_o, gin64)
 
-    if rows * cols <= 8192 * 768:
-        # accuracy against float64: the GPU form u*sigmoid(2z) must be at
-        # least as close to the exact value as the textbook float formula
-        y64 = O.bias_gelu_forward_f64(x, b)
-        gin64, _ = O.gelu_backward_with_bias_backward_f64(x, b, g)
-        e_gpu = np.abs(y - y64).max()
-        e_orc = np.abs(y_o - y64).max()
-        note(f"  fwd max err vs f64: gpu {e_gpu:.3e} oracle {e_orc:.3e}")
-        assert e_gpu <= 2 * e_orc + 1e-7
-        eg_gpu = np.abs(gin - gin64).max()
-        eg_orc = np.abs(gin_o - gin64).max()
-        note(f"  bwd max err vs f64: gpu {eg_gpu:.3e} oracle {eg_orc:.3e}")
-        assert eg_gpu <= 2 * eg_orc + 1e-7
+    e_gpu, e_orc = np.abs(y - y64).max(), np.abs(y_o - y64).max()
+    eg_gpu, eg_orc = np.abs(gin - gin64).max(), np.abs(gin_o - gin64).max()
+    note(f"  max err vs f64: fwd gpu {e_gpu:.3e} oracle {e_orc:.3e}; "
+         f"bwd gpu {eg_gpu:.3e} oracle {eg_orc:.3e}")
+    # the GPU form u*sigmoid(2z) is at least as accurate as the float formula
+    assert e_gpu <= 2 * e_orc + 1e-7
+    assert eg_gpu <= 2 * eg_orc + 1e-7
 
 
 def test_gelu_special_values(dev):
