@@ -188,32 +188,48 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void ln_bwd_group_kernel(
     }
 
     const int stride = gridDim.x * GPB;
-    int it = 0;
-    // The trip count is uniform across the workgroup (groups past the last
-    // row idle through the iteration) so the barriers below are reached by
-    // every wave.
-    for (int base_row = blockIdx.x * GPB; base_row < rows; base_row += stride, ++it) {
-        const int row = base_row + grp;
+    // One row's inputs; the next row's are loaded before the current row is
+    // processed (software pipeline), so loads stay in flight during the
+    // reductions and the dx stores.
+    struct RowIn {
+        fvec<W> go[N], xv[N];
+        float mu, is;
+    };
+    auto load_row = [&](int row, RowIn& d) {
         const bool valid = row < rows;
         const size_t off = static_cast<size_t>(valid ? row : 0) * cols;
-        fvec<W> go[N], xv[N];
 #pragma unroll
         for (int k = 0; k < N; ++k) {
             const int j = t + k * GT;
             const bool ok = valid && j < nv;
-            go[k] = ok ? sload<W>(gout + off, j) : vzero<W>();
-            xv[k] = ok ? sload<W>(x + off, j) : vzero<W>();
+            d.go[k] = ok ? sload<W>(gout + off, j) : vzero<W>();
+            d.xv[k] = ok ? sload<W>(x + off, j) : vzero<W>();
         }
-        const float mu = valid ? mean[row] : 0.0f;
-        const float is = valid ? rstd[row] : 0.0f;
+        d.mu = valid ? mean[row] : 0.0f;
+        d.is = valid ? rstd[row] : 0.0f;
+    };
+    RowIn cur, nxt;
+    int base_row = blockIdx.x * GPB;
+    load_row(base_row + grp, cur);
+    int it = 0;
+    // The trip count is uniform across the workgroup (groups past the last
+    // row idle through the iteration) so the barriers below are reached by
+    // every wave.
+    for (; base_row < rows; base_row += stride, ++it) {
+        const int row = base_row + grp;
+        const bool valid = row < rows;
+        const size_t off = static_cast<size_t>(valid ? row : 0) * cols;
+        if (base_row + stride < rows) load_row(base_row + stride + grp, nxt);
+        const float mu = cur.mu;
+        const float is = cur.is;
 
         float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
         for (int k = 0; k < N; ++k)
 #pragma unroll
             for (int e = 0; e < W; ++e) {
-                const float xh = (xv[k].v[e] - mu) * is;
-                const float dh = go[k].v[e] * gm[k].v[e];
+                const float xh = (cur.xv[k].v[e] - mu) * is;
+                const float dh = cur.go[k].v[e] * gm[k].v[e];
                 s1 += dh;
                 s2 += dh * xh;
             }
@@ -250,20 +266,22 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void ln_bwd_group_kernel(
                     if constexpr (ADD) d = sload<W>(gx + off, j);
 #pragma unroll
                     for (int e = 0; e < W; ++e) {
-                        const float xh = (xv[k].v[e] - mu) * is;
-                        const float dh = go[k].v[e] * gm[k].v[e];
+                        const float go = cur.go[k].v[e];
+                        const float xh = (cur.xv[k].v[e] - mu) * is;
+                        const float dh = go * gm[k].v[e];
                         const float dx = is * (dh - m1 - xh * m2);
                         if constexpr (ADD)
                             d.v[e] = d.v[e] + dx;
                         else
                             d.v[e] = dx;
-                        ag[k].v[e] += go[k].v[e] * xh;
-                        ab[k].v[e] += go[k].v[e];
+                        ag[k].v[e] += go * xh;
+                        ab[k].v[e] += go;
                     }
                     sstore<W>(gx + off, j, d);
                 }
             }
         }
+        cur = nxt;
     }
 
     // Combine the GPB groups' running sums: a fixed binary tree through LDS.
