@@ -269,7 +269,7 @@ struct SortPlan {
     int ntiles;
     int passes;
     size_t bytes;
-    size_t off_k1, off_v0, off_v1, off_hist;
+    size_t off_k0, off_k1, off_v0, off_v1, off_hist;
 };
 
 SortPlan plan_sort(int n, int vocab) {
@@ -283,11 +283,13 @@ SortPlan plan_sort(int n, int vocab) {
         while (bits < 32 && (1u << bits) <= static_cast<unsigned>(vocab)) ++bits;
     }
     p.passes = (bits + 7) / 8;
+    // The first 256 bytes of the workspace are reserved.
     const size_t a = round_up(static_cast<size_t>(n) * 4, 256);
-    p.off_k1 = a;
-    p.off_v0 = 2 * a;
-    p.off_v1 = 3 * a;
-    p.off_hist = 4 * a;
+    p.off_k0 = 256;
+    p.off_k1 = p.off_k0 + a;
+    p.off_v0 = p.off_k0 + 2 * a;
+    p.off_v1 = p.off_k0 + 3 * a;
+    p.off_hist = p.off_k0 + 4 * a;
     p.bytes = p.off_hist + round_up(static_cast<size_t>(p.ntiles) * kDigits * 4, 256);
     return p;
 }
@@ -397,7 +399,8 @@ int mi_embedding_backward(const float* grad_out, const int* tokens, float* grad_
     int err = MI_OK;
     char* ws = static_cast<char*>(workspace_get(p.bytes, st, &err));
     if (!ws) return err;
-    unsigned* k[2] = {reinterpret_cast<unsigned*>(ws), reinterpret_cast<unsigned*>(ws + p.off_k1)};
+    unsigned* k[2] = {reinterpret_cast<unsigned*>(ws + p.off_k0),
+                      reinterpret_cast<unsigned*>(ws + p.off_k1)};
     int* v[2] = {reinterpret_cast<int*>(ws + p.off_v0), reinterpret_cast<int*>(ws + p.off_v1)};
     int* hist = reinterpret_cast<int*>(ws + p.off_hist);
     const int n = batch_seq;

@@ -23,7 +23,7 @@
 #include "mi_common.hpp"
 
 #ifndef MI_LN_BWD_MAX_BLOCKS
-#define MI_LN_BWD_MAX_BLOCKS 512
+#define MI_LN_BWD_MAX_BLOCKS 256
 #endif
 
 namespace mi {
@@ -31,7 +31,10 @@ namespace mi {
 namespace {
 
 constexpr int kFwdWaves = 4;      // rows (waves) per forward workgroup
-constexpr int kBwdWaves = 8;      // waves per backward workgroup
+#ifndef MI_LN_BWD_WAVES
+#define MI_LN_BWD_WAVES 8
+#endif
+constexpr int kBwdWaves = MI_LN_BWD_WAVES;  // waves per backward workgroup
 constexpr int kBlockThreads = 256;  // generic block-per-row kernels
 
 // ---------------------------------------------------------------------------
@@ -510,9 +513,7 @@ void dispatch_bwd_g(const BwdPlan& p, hipStream_t st, const float* g, const floa
     }
 }
 
-size_t bwd_workspace(const BwdPlan& p, int cols) {
-    return static_cast<size_t>(p.blocks) * 2 * static_cast<size_t>(cols) * sizeof(float);
-}
+size_t bwd_workspace(const BwdPlan& p, int cols) { return colsum_bytes(p.blocks, 2 * cols); }
 
 template <bool ADD>
 int ln_backward_impl(const char* name, const float* g, const float* x, const float* m,
@@ -528,8 +529,9 @@ int ln_backward_impl(const char* name, const float* g, const float* x, const flo
                       aligned16(gx);
     const BwdPlan p = plan_bwd(rows, cols, vec4);
     int err = MI_OK;
-    float* part = static_cast<float*>(workspace_get(bwd_workspace(p, cols), st, &err));
-    if (!part) return err;
+    char* ws = static_cast<char*>(workspace_get(bwd_workspace(p, cols), st, &err));
+    if (!ws) return err;
+    float* part = reinterpret_cast<float*>(ws + colsum_part_offset());
     if (p.N) {
         if (p.W == 4)
             dispatch_bwd_g<4, ADD>(p, st, g, x, m, s, gamma, gx, part, rows, cols);

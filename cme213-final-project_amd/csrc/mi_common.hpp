@@ -132,4 +132,11 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// Workspace layout of a two-pass column reduction with P partial rows of
+// ncols floats.  The first 256 bytes of the workspace are reserved.
+inline size_t colsum_part_offset() { return 256; }
+
+inline size_t colsum_bytes(int P, int ncols) {
+    return colsum_part_offset() + static_cast<size_t>(P) * ncols * sizeof(float);
+}
 }  // namespace mi

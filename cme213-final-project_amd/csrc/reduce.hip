@@ -6,30 +6,39 @@
 // accumulates the total into the caller's gradient (the reference's `+=`
 // contract, e.g. FINAL_CLEAN_CODE/src/kernels/layernorm.cu:266-267).
 //
-// Layout: one workgroup owns 64 consecutive columns (one per lane, so each
-// partial row is read as a coalesced 256-byte segment); its 16 waves each
-// sum a contiguous slice of the P partial rows sequentially, and wave 0
-// adds the 16 slice totals in wave order.  The slice bounds depend only on
-// P, so the association order, and hence every bit of the result, is fixed.
+// Layout: one workgroup owns kFinCols consecutive columns; its threads are
+// split into kFinSlices row slices, each summing a contiguous slice of the P
+// partial rows sequentially, and the first slice adds the slice totals in
+// slice order.  The slice bounds depend only on P, so the association order,
+// and hence every bit of the result, is fixed.
 #include "mi_common.hpp"
 
 namespace mi {
 
 namespace {
 
-constexpr int kFinWaves = 16;
+#ifndef MI_FIN_WAVES
+#define MI_FIN_WAVES 16
+#endif
+#ifndef MI_FIN_COLS
+#define MI_FIN_COLS 64
+#endif
+constexpr int kFinWaves = MI_FIN_WAVES;
+constexpr int kFinThreads = kFinWaves * kWave;
+constexpr int kFinCols = MI_FIN_COLS;                 // columns per workgroup
+constexpr int kFinSlices = kFinThreads / kFinCols;    // row slices per workgroup
 constexpr int kChunk = 32;
 
-__global__ __launch_bounds__(kFinWaves * kWave) void colsum_finalize_kernel(
+__global__ __launch_bounds__(kFinThreads) void colsum_finalize_kernel(
     const float* __restrict__ part, int P, int ncols, float* __restrict__ out0, int split,
     float* __restrict__ out1) {
-    __shared__ float tot[kFinWaves][kWave];
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    const int c = blockIdx.x * kWave + lane;
-    const int p0 = static_cast<int>(static_cast<long long>(wave) * P / kFinWaves);
-    const int p1 = static_cast<int>(static_cast<long long>(wave + 1) * P / kFinWaves);
-    // All loads of a chunk are issued before the first add, so a wave waits
+    __shared__ float tot[kFinSlices][kFinCols];
+    const int cl = threadIdx.x % kFinCols;
+    const int slice = threadIdx.x / kFinCols;
+    const int c = blockIdx.x * kFinCols + cl;
+    const int p0 = static_cast<int>(static_cast<long long>(slice) * P / kFinSlices);
+    const int p1 = static_cast<int>(static_cast<long long>(slice + 1) * P / kFinSlices);
+    // All loads of a chunk are issued before the first add, so a thread waits
     // for one memory round trip per kChunk partial rows.
     float s = 0.0f;
     if (c < ncols) {
@@ -44,12 +53,12 @@ __global__ __launch_bounds__(kFinWaves * kWave) void colsum_finalize_kernel(
                 if (pb + k < p1) s += v[k];
         }
     }
-    tot[wave][lane] = s;
+    tot[slice][cl] = s;
     __syncthreads();
-    if (wave == 0 && c < ncols) {
-        float t = tot[0][lane];
+    if (slice == 0 && c < ncols) {
+        float t = tot[0][cl];
 #pragma unroll
-        for (int w = 1; w < kFinWaves; ++w) t += tot[w][lane];
+        for (int w = 1; w < kFinSlices; ++w) t += tot[w][cl];
         float* o = (c < split) ? (out0 + c) : (out1 + (c - split));
         *o = *o + t;
     }
@@ -60,8 +69,8 @@ __global__ __launch_bounds__(kFinWaves * kWave) void colsum_finalize_kernel(
 int launch_colsum_finalize(const float* part, int P, int ncols, float* out0, int split,
                            float* out1, hipStream_t stream) {
     if (ncols <= 0 || P <= 0) return MI_OK;
-    const int grid = (ncols + kWave - 1) / kWave;
-    hipLaunchKernelGGL(colsum_finalize_kernel, dim3(grid), dim3(kFinWaves * kWave), 0, stream,
+    const int grid = (ncols + kFinCols - 1) / kFinCols;
+    hipLaunchKernelGGL(colsum_finalize_kernel, dim3(grid), dim3(kFinThreads), 0, stream,
                        part, P, ncols, out0, split, out1);
     return check_launch("colsum_finalize");
 }

@@ -62,10 +62,11 @@ def test_host_side_argument_errors():
 
 
 def test_workspace_size_queries():
+    # counters (256 B) + group rows + partial rows, at most 512 partial rows
     ln = M.lib.mi_layernorm_backward_workspace(8192, 768)
-    assert 0 < ln <= 512 * 2 * 768 * 4
+    assert 2 * 768 * 4 < ln <= 256 + (512 + 32) * 2 * 768 * 4 + 256
     gb = M.lib.mi_bias_backward_workspace(8192, 3072)
-    assert 0 < gb <= 512 * 3072 * 4
+    assert 3072 * 4 < gb <= 256 + (512 + 32) * 3072 * 4 + 256
     eb = M.lib.mi_embedding_backward_workspace(16384)
     assert eb >= 4 * 16384 * 4
     assert M.lib.mi_layernorm_backward_workspace(0, 768) == 0
