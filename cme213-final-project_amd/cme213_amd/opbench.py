@@ -1,0 +1,67 @@
+"""Runs each operation of the headline step (and a copy kernel of known size)
+a few times with the last-level cache flushed before each call, for
+rocprofv3 counter collection, e.g.
+
+  rocprofv3 --pmc FETCH_SIZE -d OUT -o pmc -- \
+      python3 cme213-final-project_amd/cme213_amd/opbench.py
+
+The copy kernel (relu_forward over [8192, 3072]: 96 MiB read, 96 MiB
+written) calibrates what the counters read for a known number of bytes.
+"""
+import argparse
+import os
+import sys
+
+sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+
+import torch  # noqa: E402
+
+import cme213_amd as M  # noqa: E402
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--iters", type=int, default=3)
+    args = ap.parse_args()
+    R, C, F = 8192, 768, 3072
+    g = torch.Generator(device="cuda")
+    g.manual_seed(3)
+
+    def rn(*s):
+        return torch.randn(*s, device="cuda", generator=g)
+
+    x, dy = rn(R, C), rn(R, C)
+    y, dx = torch.empty(R, C, device="cuda"), torch.empty(R, C, device="cuda")
+    m, s = torch.empty(R, device="cuda"), torch.empty(R, device="cuda")
+    h, dh = rn(R, F), rn(R, F)
+    o, gin = torch.empty(R, F, device="cuda"), torch.empty(R, F, device="cuda")
+    gm, bt, bias = rn(C) * 0.02 + 1, rn(C) * 0.02, rn(F) * 0.02
+    dg, db, dbi = (torch.zeros(C, device="cuda"), torch.zeros(C, device="cuda"),
+                   torch.zeros(F, device="cuda"))
+    flush_src = torch.empty(128 << 20, device="cuda")  # 512 MiB, twice the last-level cache
+    flush_dst = torch.empty_like(flush_src)
+
+    def flush():
+        flush_dst.copy_(flush_src)
+        torch.cuda.synchronize()
+
+    calls = [
+        ("copy relu_forward [8192,3072]", lambda: M.relu_forward(h, o, R * F)),
+        ("layernorm_forward_save [8192,768]",
+         lambda: M.layernorm_forward_save(x, gm, bt, y, m, s, R, C)),
+        ("layernorm_backward [8192,768]",
+         lambda: M.layernorm_backward(dy, x, m, s, gm, dx, dg, db, R, C)),
+        ("bias_gelu_forward [8192,3072]", lambda: M.bias_gelu_forward(h, bias, o, R, F)),
+        ("gelu_backward_with_bias_backward [8192,3072]",
+         lambda: M.gelu_backward_with_bias_backward(h, bias, dh, gin, dbi, R, F)),
+    ]
+    for _ in range(args.iters):
+        for name, fn in calls:
+            flush()
+            fn()
+            torch.cuda.synchronize()
+    print("opbench: ran", ", ".join(n for n, _ in calls), flush=True)
+
+
+if __name__ == "__main__":
+    main()

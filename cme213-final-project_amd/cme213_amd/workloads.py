@@ -57,58 +57,83 @@ def _randn(shape, gen, scale=1.0, shift=0.0):
     return t
 
 
-class Headline:
-    """LN fwd+bwd on [R, C] and bias+GELU fwd+bwd on [R, F] (BASELINE metric,
-    B=8, T=1024, C=768, F=4C).
+def _sets_for(set_bytes, min_sets=2, target=1.2e9, max_sets=32):
+    """Number of buffer sets so that about `target` bytes of other data pass
+    between two uses of the same set (more than the 256 MB last-level cache)."""
+    n = int(-(-target // max(set_bytes, 1)))
+    return max(min_sets, min(max_sets, n))
 
-    `sets` independent buffer sets rotate.  Step k runs the two forward
-    operations on set k and the two backward operations on set k-1, whose
-    forward ran one step earlier (as in training, where a layer's backward
-    comes long after its forward).  Between two reads of any input tensor
-    at least ~800 MB of other data is streamed, more than the 256 MB
-    last-level cache, so every operation reads its inputs from HBM."""
 
-    def __init__(self, R=8192, C=768, F=3072, sets=4, seed=20260):
+class FwdBwd:
+    """LayerNorm fwd+bwd on [R, C] and/or bias+GELU fwd+bwd on [R, F].
+
+    The BASELINE headline metric is FwdBwd(8192, 768, 3072) (B=8, T=1024,
+    C=768, F=4C); config 0 is the LayerNorm half at R=4096, config 1 the GELU
+    half, config 4's wide sweep the LayerNorm half at [32768, 4096].
+
+    Independent buffer sets rotate.  Step k runs the forward operations on
+    set k and the backward operations on set k-1, whose forward ran one step
+    earlier (as in training, where a layer's backward comes long after its
+    forward).  Enough sets are used that ~1.2 GB of other data streams
+    between two reads of any input, more than the 256 MB last-level cache,
+    so every operation reads its inputs from HBM."""
+
+    def __init__(self, R=8192, C=768, F=3072, ln=True, gelu=True, sets=None, seed=20260):
         self.R, self.C, self.F = R, C, F
+        self.ln, self.gelu = ln, gelu
         g = torch.Generator(device="cuda")
         g.manual_seed(seed)
-        self.gamma = _randn((C,), g, 0.02, 1.0)
-        self.beta = _randn((C,), g, 0.02)
-        self.bias = _randn((F,), g, 0.02)
-        self.dgamma = torch.zeros(C, device="cuda")
-        self.dbeta = torch.zeros(C, device="cuda")
-        self.dbias = torch.zeros(F, device="cuda")
+        self.bytes = {}
+        if ln:
+            self.bytes["ln_fwd"] = ln_fwd_bytes(R, C)
+            self.bytes["ln_bwd"] = ln_bwd_bytes(R, C)
+            self.gamma = _randn((C,), g, 0.02, 1.0)
+            self.beta = _randn((C,), g, 0.02)
+            self.dgamma = torch.zeros(C, device="cuda")
+            self.dbeta = torch.zeros(C, device="cuda")
+        if gelu:
+            self.bytes["gelu_fwd"] = gelu_fwd_bytes(R, F)
+            self.bytes["gelu_bwd"] = gelu_bwd_bytes(R, F)
+            self.bias = _randn((F,), g, 0.02)
+            self.dbias = torch.zeros(F, device="cuda")
+        set_bytes = F32 * R * ((4 * C if ln else 0) + (4 * F if gelu else 0))
+        n = sets if sets is not None else _sets_for(set_bytes, min_sets=4)
         self.sets = []
-        for _ in range(sets):
-            s = {
-                "x": _randn((R, C), g), "dy": _randn((R, C), g),
-                "h": _randn((R, F), g, 1.5), "dh": _randn((R, F), g),
-                "y": torch.empty(R, C, device="cuda"), "dx": torch.empty(R, C, device="cuda"),
-                "mean": torch.empty(R, device="cuda"), "rstd": torch.empty(R, device="cuda"),
-                "o": torch.empty(R, F, device="cuda"), "gin": torch.empty(R, F, device="cuda"),
-            }
+        for _ in range(n):
+            s = {}
+            if ln:
+                s.update(x=_randn((R, C), g), dy=_randn((R, C), g),
+                         y=torch.empty(R, C, device="cuda"), dx=torch.empty(R, C, device="cuda"),
+                         mean=torch.empty(R, device="cuda"), rstd=torch.empty(R, device="cuda"))
+            if gelu:
+                s.update(h=_randn((R, F), g, 1.5), dh=_randn((R, F), g),
+                         o=torch.empty(R, F, device="cuda"), gin=torch.empty(R, F, device="cuda"))
             self.sets.append(s)
-        self.bytes = headline_bytes(R, C, F)
         self.step_bytes = sum(self.bytes.values())
-        for s in self.sets:  # every set's saved statistics exist before its backward
-            layernorm_forward_save(s["x"], self.gamma, self.beta, s["y"], s["mean"], s["rstd"],
-                                   R, C, 1e-5)
+        if ln:
+            for s in self.sets:  # every set's saved statistics exist before its backward
+                layernorm_forward_save(s["x"], self.gamma, self.beta, s["y"], s["mean"],
+                                       s["rstd"], R, C, 1e-5)
 
     def ops(self, k):
         n = len(self.sets)
         f = self.sets[k % n]
         b = self.sets[(k - 1) % n]
         R, C, F = self.R, self.C, self.F
-        return [
-            ("ln_fwd", lambda: layernorm_forward_save(f["x"], self.gamma, self.beta, f["y"],
-                                                      f["mean"], f["rstd"], R, C, 1e-5)),
-            ("gelu_fwd", lambda: bias_gelu_forward(f["h"], self.bias, f["o"], R, F)),
-            ("ln_bwd", lambda: layernorm_backward(b["dy"], b["x"], b["mean"], b["rstd"],
-                                                  self.gamma, b["dx"], self.dgamma, self.dbeta,
-                                                  R, C)),
-            ("gelu_bwd", lambda: gelu_backward_with_bias_backward(b["h"], self.bias, b["dh"],
-                                                                   b["gin"], self.dbias, R, F)),
-        ]
+        out = []
+        if self.ln:
+            out.append(("ln_fwd", lambda: layernorm_forward_save(
+                f["x"], self.gamma, self.beta, f["y"], f["mean"], f["rstd"], R, C, 1e-5)))
+        if self.gelu:
+            out.append(("gelu_fwd", lambda: bias_gelu_forward(f["h"], self.bias, f["o"], R, F)))
+        if self.ln:
+            out.append(("ln_bwd", lambda: layernorm_backward(
+                b["dy"], b["x"], b["mean"], b["rstd"], self.gamma, b["dx"], self.dgamma,
+                self.dbeta, R, C)))
+        if self.gelu:
+            out.append(("gelu_bwd", lambda: gelu_backward_with_bias_backward(
+                b["h"], self.bias, b["dh"], b["gin"], self.dbias, R, F)))
+        return out
 
     def step(self, k):
         for _, fn in self.ops(k):
@@ -116,9 +141,18 @@ class Headline:
 
     def host_inputs(self, k=0):
         s = self.sets[k % len(self.sets)]
-        return {n: t.cpu().numpy() for n, t in
-                [("x", s["x"]), ("dy", s["dy"]), ("h", s["h"]), ("dh", s["dh"]),
-                 ("gamma", self.gamma), ("beta", self.beta), ("bias", self.bias)]}
+        d = {n: t.cpu().numpy() for n, t in s.items()
+             if n in ("x", "dy", "h", "dh")}
+        if self.ln:
+            d.update(gamma=self.gamma.cpu().numpy(), beta=self.beta.cpu().numpy())
+        if self.gelu:
+            d.update(bias=self.bias.cpu().numpy())
+        return d
+
+
+def Headline(sets=None):
+    """The BASELINE metric's workload."""
+    return FwdBwd(8192, 768, 3072, sets=sets)
 
 
 class BlockSequence:
@@ -155,6 +189,16 @@ class BlockSequence:
     def _in(self, l):
         return self.inp[l % len(self.inp)]
 
+    def step(self, k):
+        """One training step's non-GEMM work: forward over all layers, then
+        backward over all layers (a fixed upstream gradient)."""
+        if not hasattr(self, "gtop"):
+            g = torch.Generator(device="cuda")
+            g.manual_seed(11)
+            self.gtop = _randn((self.R, self.C), g)
+        self.forward()
+        self.backward(self.gtop)
+
     def forward(self):
         R, C, F = self.R, self.C, self.F
         r = self.r0
@@ -184,27 +228,40 @@ class BlockSequence:
 
 
 class Embedding:
-    """ids U[0, V) for B x T, wte [V, D], wpe [T, D]."""
+    """ids U[0, V) for B x T, wte [V, D], wpe [T, D].
+    `sets` independent id / gradient / output sets rotate between steps."""
 
-    def __init__(self, V=50257, D=768, B=16, T=1024, seed=20262):
+    def __init__(self, V=50257, D=768, B=16, T=1024, sets=4, seed=20262):
         self.V, self.D, self.B, self.T = V, D, B, T
         g = torch.Generator(device="cuda")
         g.manual_seed(seed)
         self.wte = _randn((V, D), g, 0.02)
         self.wpe = _randn((T, D), g, 0.02)
-        self.ids = torch.randint(0, V, (B * T,), device="cuda", generator=g, dtype=torch.int32)
-        self.dout = _randn((B * T, D), g)
-        self.out = torch.empty(B * T, D, device="cuda")
         self.dwte = torch.zeros(V, D, device="cuda")
         self.dwpe = torch.zeros(T, D, device="cuda")
-        self.distinct = int(torch.unique(self.ids).numel())
         BT = B * T
+        self.sets = []
+        for _ in range(sets):
+            ids = torch.randint(0, V, (BT,), device="cuda", generator=g, dtype=torch.int32)
+            self.sets.append({"ids": ids, "dout": _randn((BT, D), g),
+                              "out": torch.empty(BT, D, device="cuda"),
+                              "distinct": int(torch.unique(ids).numel())})
+        self.distinct = sum(s["distinct"] for s in self.sets) / len(self.sets)
         self.fwd_bytes = F32 * (BT + 2 * BT * D + T * D)
-        self.bwd_bytes = F32 * (BT * D + BT + 2 * self.distinct * D + 2 * T * D)
+        self.bwd_bytes = int(F32 * (BT * D + BT + 2 * self.distinct * D + 2 * T * D))
+        self.bytes = {"emb_fwd": self.fwd_bytes, "emb_bwd": self.bwd_bytes}
+        self.step_bytes = self.fwd_bytes + self.bwd_bytes
 
-    def forward(self):
-        embedding_pos_forward(self.wte, self.wpe, self.ids, self.out, self.B, self.T, self.D, self.V)
+    def ops(self, k):
+        s = self.sets[k % len(self.sets)]
+        B, T, D, V = self.B, self.T, self.D, self.V
+        return [
+            ("emb_fwd", lambda: embedding_pos_forward(self.wte, self.wpe, s["ids"], s["out"], B, T,
+                                                      D, V)),
+            ("emb_bwd", lambda: (embedding_backward(s["dout"], s["ids"], self.dwte, B * T, D, V),
+                                 pos_embedding_backward(s["dout"], self.dwpe, B, T, D))),
+        ]
 
-    def backward(self):
-        embedding_backward(self.dout, self.ids, self.dwte, self.B * self.T, self.D, self.V)
-        pos_embedding_backward(self.dout, self.dwpe, self.B, self.T, self.D)
+    def step(self, k):
+        for _, fn in self.ops(k):
+            fn()

@@ -1,8 +1,11 @@
 """Tolerances of the parity tests (stated once, used everywhere).
 
 Forward fp32 outputs (LayerNorm y, GELU y):      |gpu - ref| <= 1e-6 + 1e-5 |ref|
-Element-wise backward outputs (dx, grad_in):     |gpu - ref| <= 1e-6 s + 1e-4 |ref|,
+Element-wise backward outputs (dx, grad_in):     |gpu - ref| <= 1e-5 s + 1e-4 |ref|,
                                                  s = max(1, rms(ref))
+    (the near-zero floor 1e-5 s covers gradients that are cancelling sums of
+    O(1) terms, e.g. the residual-stream gradient gtop + dx2 + dx1, whose
+    fp32 rounding is ~1e-6 absolute while the value itself may be ~1e-3)
 Column sums (dgamma, dbeta, dbias):              |gpu - ref| <= 1e-4 (|ref| + ||t_c||_2)
     where t_c are the per-row terms summed into column c; the float error of
     any summation order scales with ||t_c||_2, so a column whose sum cancels
@@ -17,7 +20,7 @@ also held to the plain tolerance against the float64 oracle.
 import numpy as np
 
 FWD_RTOL, FWD_ATOL = 1e-5, 1e-6
-BWD_RTOL, BWD_ATOL = 1e-4, 1e-6
+BWD_RTOL, BWD_ATOL = 1e-4, 1e-5
 COL_RTOL = 1e-4
 
 
