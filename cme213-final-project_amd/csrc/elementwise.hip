@@ -160,11 +160,15 @@ int launch_flat(const char* name, Op op, long long nvec, hipStream_t st) {
 // size), so at any moment the resident workgroups stream one contiguous band
 // of rows and HBM sees a linear sweep.  Rows are processed in batches of
 // kUnroll, with the next batch's loads issued before the current batch is
-// computed (software pipeline).
+// computed (software pipeline).  Rows wider than 4 x 1024 vectors use the
+// column-slice fallback below.
 // ---------------------------------------------------------------------------
 template <int W, int NC, class Op, bool REDUCE>
 __global__ __launch_bounds__(1024) void rowband_kernel(Op op, const float* __restrict__ bias,
                                                        float* __restrict__ part, int rows, int nv) {
+    // Pipeline depth shrinks as the per-thread width grows, so the buffers
+    // stay within the 128 VGPRs a 1024-thread workgroup allows (no spills).
+    constexpr int U = NC == 1 ? kUnroll : (NC == 2 ? 2 : 1);
     const int T = blockDim.x;
     const int G = gridDim.x;
     fvec<W> bv[NC], acc[NC];
@@ -174,10 +178,10 @@ __global__ __launch_bounds__(1024) void rowband_kernel(Op op, const float* __res
         bv[k] = (bias && j < nv) ? vload<W>(bias, j) : vzero<W>();
         acc[k] = vzero<W>();
     }
-    typename Op::In cur[kUnroll][NC], nxt[kUnroll][NC];
-    auto load_batch = [&](int r, typename Op::In (&d)[kUnroll][NC]) {
+    typename Op::In cur[U][NC], nxt[U][NC];
+    auto load_batch = [&](int r, typename Op::In (&d)[U][NC]) {
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
+        for (int u = 0; u < U; ++u) {
             const int row = r + u * G;
             if (row < rows) {
 #pragma unroll
@@ -188,13 +192,16 @@ __global__ __launch_bounds__(1024) void rowband_kernel(Op op, const float* __res
             }
         }
     };
-    const int step = kUnroll * G;
+    // Widths of 3+ vectors per thread already keep several loads in flight;
+    // they skip the prefetch buffer to stay spill-free.
+    constexpr bool kPrefetch = NC <= 2;
+    const int step = U * G;
     int r = blockIdx.x;
     load_batch(r, cur);
     for (; r < rows; r += step) {
-        if (r + step < rows) load_batch(r + step, nxt);
+        if (kPrefetch && r + step < rows) load_batch(r + step, nxt);
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
+        for (int u = 0; u < U; ++u) {
             const int row = r + u * G;
             if (row < rows) {
 #pragma unroll
@@ -211,10 +218,14 @@ __global__ __launch_bounds__(1024) void rowband_kernel(Op op, const float* __res
                 }
             }
         }
+        if constexpr (kPrefetch) {
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u)
+            for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int k = 0; k < NC; ++k) cur[u][k] = nxt[u][k];
+                for (int k = 0; k < NC; ++k) cur[u][k] = nxt[u][k];
+        } else if (r + step < rows) {
+            load_batch(r + step, cur);
+        }
     }
     if constexpr (REDUCE) {
         float* prow = part + static_cast<size_t>(blockIdx.x) * nv * W;
@@ -429,7 +440,7 @@ struct BandShape {
     int threads;
 };
 
-constexpr int kMaxNC = 8;
+constexpr int kMaxNC = 4;
 
 BandShape band_shape(int nv) {
     int nc = (nv + 1023) / 1024;
@@ -457,10 +468,6 @@ void launch_band(const BandShape& b, int grid, Op op, const float* bias, float* 
         MI_BAND_CASE(2)
         MI_BAND_CASE(3)
         MI_BAND_CASE(4)
-        MI_BAND_CASE(5)
-        MI_BAND_CASE(6)
-        MI_BAND_CASE(7)
-        MI_BAND_CASE(8)
         default:
             break;
     }

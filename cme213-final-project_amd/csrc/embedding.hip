@@ -13,9 +13,10 @@
 //   1. keys = ids (invalid ids -> a sentinel that sorts last), vals = i;
 //   2. stable LSD radix sort of (key, val), 8-bit digits, only as many
 //      passes as the key range needs.  Each pass: per-tile digit histogram
-//      (LDS integer counters), one exclusive scan over (digit, tile), and a
-//      stable scatter where one wave ranks its tile's elements 64 at a time
-//      in index order (ballot-based digit match + popcount);
+//      (256-element tiles, LDS integer counters), a scan over tiles per
+//      digit, and a stable scatter where one wave ranks its tile's
+//      elements 64 at a time in index order (ballot-based digit match +
+//      popcount).  Pass 0 reads the ids themselves;
 //   3. one wave per run of equal keys: load grad_table[key] once, add the
 //      run's grad rows in sorted (= increasing i) order, store once.
 // Position backward: one thread per (t, column vector) adds grad_out[b, t]
@@ -27,9 +28,11 @@ namespace mi {
 namespace {
 
 constexpr int kRowWaves = 4;   // token rows per workgroup
-constexpr int kTile = 1024;    // radix tile: 16 batches of 64
+constexpr int kTile = 256;     // radix tile: 4 batches of 64, one wave
 constexpr int kDigits = 256;
 constexpr unsigned kSentinel = 0xFFFFFFFFu;
+static_assert(kTile == kDigits, "radix_hist_kernel uses one thread per digit and per element");
+static_assert(kDigits == 4 * kWave, "radix_scatter_kernel scans four digit totals per lane");
 
 // ---------------------------------------------------------------------------
 // Forward
@@ -112,48 +115,48 @@ __global__ __launch_bounds__(256) void pos_bwd_kernel(const float* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------
-// Stable LSD radix sort of (key, val) pairs.
+// Stable LSD radix sort of (key, val) pairs.  Pass 0 reads the token ids
+// directly (key = id, or the sentinel for an invalid id; val = position).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void prep_keys_kernel(const int* __restrict__ ids,
-                                                        unsigned* __restrict__ keys,
-                                                        int* __restrict__ vals, int n, int vocab) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= n) return;
-    const int id = ids[i];
+__device__ __forceinline__ unsigned token_key(int id, int vocab) {
     const bool ok = id >= 0 && (vocab <= 0 || id < vocab);
-    keys[i] = ok ? static_cast<unsigned>(id) : kSentinel;
-    vals[i] = i;
+    return ok ? static_cast<unsigned>(id) : kSentinel;
 }
 
 // hist[d * ntiles + tile] = number of keys of the tile whose digit is d.
-__global__ __launch_bounds__(256) void radix_hist_kernel(const unsigned* __restrict__ keys, int n,
-                                                         int shift, int ntiles,
-                                                         int* __restrict__ hist) {
+// One 256-thread workgroup per tile, one element per thread.
+__global__ __launch_bounds__(kTile) void radix_hist_kernel(const unsigned* __restrict__ keys,
+                                                           const int* __restrict__ ids, int vocab,
+                                                           int n, int shift, int ntiles,
+                                                           int* __restrict__ hist) {
     __shared__ int cnt[kDigits];
     cnt[threadIdx.x] = 0;
     __syncthreads();
-    const int base = blockIdx.x * kTile;
-    for (int k = threadIdx.x; k < kTile; k += 256) {
-        const int e = base + k;
-        if (e < n) atomicAdd(&cnt[(keys[e] >> shift) & (kDigits - 1)], 1);
+    const int e = blockIdx.x * kTile + threadIdx.x;
+    if (e < n) {
+        const unsigned key = ids ? token_key(ids[e], vocab) : keys[e];
+        atomicAdd(&cnt[(key >> shift) & (kDigits - 1)], 1);
     }
     __syncthreads();
     hist[threadIdx.x * ntiles + blockIdx.x] = cnt[threadIdx.x];
 }
 
-// In-place exclusive scan of m ints by one 1024-thread workgroup.
-__global__ __launch_bounds__(1024) void exclusive_scan_kernel(int* __restrict__ data, int m) {
-    __shared__ int wsum[16];
+// Per-digit scan over tiles: hist[d * ntiles + t] becomes the number of
+// digit-d keys in tiles before t, and total[d] the number of digit-d keys.
+// One 256-thread workgroup per digit (the row of one digit is contiguous).
+__global__ __launch_bounds__(256) void digit_scan_kernel(int* __restrict__ hist,
+                                                         int* __restrict__ total, int ntiles) {
+    __shared__ int wsum[4];
     __shared__ int carry_s;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
+    int* h = hist + static_cast<size_t>(blockIdx.x) * ntiles;
     if (threadIdx.x == 0) carry_s = 0;
     __syncthreads();
-    for (int base = 0; base < m; base += 1024) {
+    for (int base = 0; base < ntiles; base += 256) {
         const int i = base + threadIdx.x;
-        const int v = i < m ? data[i] : 0;
-        // inclusive wave scan (Hillis-Steele over 64 lanes)
-        int x = v;
+        const int v = i < ntiles ? h[i] : 0;
+        int x = v;  // inclusive scan over the wave
 #pragma unroll
         for (int off = 1; off < kWave; off <<= 1) {
             const int y = __shfl_up(x, off, kWave);
@@ -163,44 +166,82 @@ __global__ __launch_bounds__(1024) void exclusive_scan_kernel(int* __restrict__ 
         __syncthreads();
         int before = carry_s;
         for (int w = 0; w < wave; ++w) before += wsum[w];
-        if (i < m) data[i] = before + x - v;
+        if (i < ntiles) h[i] = before + x - v;
         __syncthreads();
-        if (threadIdx.x == 1023) carry_s = before + x;
+        if (threadIdx.x == 255) carry_s = before + x;
         __syncthreads();
     }
+    if (threadIdx.x == 0) total[blockIdx.x] = carry_s;
 }
 
-// Stable scatter of one tile by one wave; offs = scanned hist.
+// Stable scatter of one tile (kTile elements, 64 at a time in index order)
+// by one wave.  The output position of digit d starts at
+// (number of keys with a smaller digit) + offs[d * ntiles + tile]; the first
+// term is an exclusive scan of the 256 digit totals, done by the wave (four
+// digits per lane).
 __global__ __launch_bounds__(kWave) void radix_scatter_kernel(
-    const unsigned* __restrict__ kin, const int* __restrict__ vin, unsigned* __restrict__ kout,
-    int* __restrict__ vout, int n, int shift, int ntiles, const int* __restrict__ offs) {
+    const unsigned* __restrict__ kin, const int* __restrict__ vin, const int* __restrict__ ids,
+    int vocab, unsigned* __restrict__ kout, int* __restrict__ vout, int n, int shift, int ntiles,
+    const int* __restrict__ offs, const int* __restrict__ total) {
     __shared__ int run[kDigits];
     const int lane = threadIdx.x;
     const int tile = blockIdx.x;
+    {
+        int t[4], sum = 0;
 #pragma unroll
-    for (int d = lane; d < kDigits; d += kWave) run[d] = offs[d * ntiles + tile];
+        for (int k = 0; k < 4; ++k) {
+            t[k] = total[4 * lane + k];
+            sum += t[k];
+        }
+        int x = sum;  // inclusive scan of the per-lane sums
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {
+            const int y = __shfl_up(x, off, kWave);
+            if (lane >= off) x += y;
+        }
+        int base = x - sum;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int d = 4 * lane + k;
+            run[d] = base + offs[d * ntiles + tile];
+            base += t[k];
+        }
+    }
+    // All of the tile's keys and values are loaded before the ranking.
+    unsigned key[kTile / kWave];
+    int val[kTile / kWave];
+#pragma unroll
+    for (int b = 0; b < kTile / kWave; ++b) {
+        const int e = tile * kTile + b * kWave + lane;
+        if (e < n) {
+            key[b] = ids ? token_key(ids[e], vocab) : kin[e];
+            val[b] = ids ? e : vin[e];
+        } else {
+            key[b] = 0u;
+            val[b] = 0;
+        }
+    }
     __syncthreads();
     const unsigned long long below = (1ull << lane) - 1ull;
+#pragma unroll
     for (int b = 0; b < kTile / kWave; ++b) {
         const int e = tile * kTile + b * kWave + lane;
         const bool valid = e < n;
-        const unsigned key = valid ? kin[e] : 0u;
-        const int val = valid ? vin[e] : 0;
-        const int d = static_cast<int>((key >> shift) & (kDigits - 1));
+        const int d = static_cast<int>((key[b] >> shift) & (kDigits - 1));
         unsigned long long peers = __ballot(valid);
 #pragma unroll
         for (int bit = 0; bit < 8; ++bit) {
             const bool set = (d >> bit) & 1;
-            const unsigned long long m = __ballot(set);
-            peers &= set ? m : ~m;
+            const unsigned long long msk = __ballot(set);
+            peers &= set ? msk : ~msk;
         }
         const int rank = __popcll(peers & below);
         const int pos = run[d] + rank;
         const bool leader = valid && (63 - __clzll(peers)) == lane;
         __syncthreads();  // every lane has read run[] before the leaders update it
         if (valid) {
-            kout[pos] = key;
-            vout[pos] = val;
+            kout[pos] = key[b];
+            vout[pos] = val[b];
         }
         if (leader) run[d] += __popcll(peers);
         __syncthreads();
@@ -209,6 +250,10 @@ __global__ __launch_bounds__(kWave) void radix_scatter_kernel(
 
 // One wave per sorted position; the first position of each run of equal
 // keys accumulates the run's grad rows, in sorted order, onto its table row.
+// The table row, the run's keys and its values are requested together; the
+// grad rows are then loaded kAccBatch at a time before being added in order.
+constexpr int kAccBatch = 4;
+
 template <int W, int NCH>
 __global__ __launch_bounds__(kRowWaves * kWave) void emb_bwd_accum_kernel(
     const unsigned* __restrict__ keys, const int* __restrict__ vals, int n,
@@ -219,18 +264,6 @@ __global__ __launch_bounds__(kRowWaves * kWave) void emb_bwd_accum_kernel(
     const unsigned key = keys[s];
     if (key == kSentinel) return;
     if (s > 0 && keys[s - 1] == key) return;
-    // Find the end of the run, 64 keys at a time.
-    int end = s + 1;
-    for (;;) {
-        const int e = end + lane;
-        const bool same = e < n && keys[e] == key;
-        const unsigned long long m = __ballot(same);
-        const unsigned long long miss = ~m;
-        const int first_miss =
-            miss ? __ffsll(static_cast<unsigned long long>(miss)) - 1 : kWave;  // 0..64
-        end += first_miss;
-        if (first_miss < kWave) break;
-    }
     const int nv = dim / W;
     float* trow = table + static_cast<size_t>(key) * dim;
     for (int c0 = 0; c0 < nv; c0 += NCH * kWave) {
@@ -240,22 +273,48 @@ __global__ __launch_bounds__(kRowWaves * kWave) void emb_bwd_accum_kernel(
             const int j = c0 + lane + k * kWave;
             acc[k] = j < nv ? vload<W>(trow, j) : vzero<W>();
         }
-        for (int b0 = s; b0 < end; b0 += kWave) {
-            const int cnt = min(kWave, end - b0);
-            const int my_i = (b0 + lane < end) ? vals[b0 + lane] : 0;
-            for (int q = 0; q < cnt; ++q) {
-                const int i = __shfl(my_i, q, kWave);
-                const float* grow = g + static_cast<size_t>(i) * dim;
+        // Walk the run 64 positions at a time; a chunk's keys tell where the
+        // run ends, its values which grad rows to add.
+        for (int b0 = s;; b0 += kWave) {
+            const int e = b0 + lane;
+            const bool same = e < n && keys[e] == key;
+            const int my_i = same ? vals[e] : 0;
+            const unsigned long long m = __ballot(same);
+            // the run is contiguous from b0, so its length in this chunk is
+            // the number of trailing set bits
+            const int cnt = (~m == 0ull) ? kWave : (__ffsll(static_cast<unsigned long long>(~m)) - 1);
+            int q = 0;
+            for (; q + kAccBatch <= cnt; q += kAccBatch) {
+                fvec<W> v[kAccBatch][NCH];
+#pragma unroll
+                for (int u = 0; u < kAccBatch; ++u) {
+                    const float* grow = g + static_cast<size_t>(__shfl(my_i, q + u, kWave)) * dim;
+#pragma unroll
+                    for (int k = 0; k < NCH; ++k) {
+                        const int j = c0 + lane + k * kWave;
+                        v[u][k] = j < nv ? vload<W>(grow, j) : vzero<W>();
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < kAccBatch; ++u)
+#pragma unroll
+                    for (int k = 0; k < NCH; ++k)
+#pragma unroll
+                        for (int x = 0; x < W; ++x) acc[k].v[x] = acc[k].v[x] + v[u][k].v[x];
+            }
+            for (; q < cnt; ++q) {
+                const float* grow = g + static_cast<size_t>(__shfl(my_i, q, kWave)) * dim;
 #pragma unroll
                 for (int k = 0; k < NCH; ++k) {
                     const int j = c0 + lane + k * kWave;
                     if (j < nv) {
                         const fvec<W> v = vload<W>(grow, j);
 #pragma unroll
-                        for (int e = 0; e < W; ++e) acc[k].v[e] = acc[k].v[e] + v.v[e];
+                        for (int x = 0; x < W; ++x) acc[k].v[x] = acc[k].v[x] + v.v[x];
                     }
                 }
             }
+            if (cnt < kWave) break;
         }
 #pragma unroll
         for (int k = 0; k < NCH; ++k) {
@@ -269,7 +328,7 @@ struct SortPlan {
     int ntiles;
     int passes;
     size_t bytes;
-    size_t off_k0, off_k1, off_v0, off_v1, off_hist;
+    size_t off_k0, off_k1, off_v0, off_v1, off_hist, off_total;
 };
 
 SortPlan plan_sort(int n, int vocab) {
@@ -290,7 +349,8 @@ SortPlan plan_sort(int n, int vocab) {
     p.off_v0 = p.off_k0 + 2 * a;
     p.off_v1 = p.off_k0 + 3 * a;
     p.off_hist = p.off_k0 + 4 * a;
-    p.bytes = p.off_hist + round_up(static_cast<size_t>(p.ntiles) * kDigits * 4, 256);
+    p.off_total = p.off_hist + round_up(static_cast<size_t>(p.ntiles) * kDigits * 4, 256);
+    p.bytes = p.off_total + kDigits * 4;
     return p;
 }
 
@@ -403,19 +463,20 @@ int mi_embedding_backward(const float* grad_out, const int* tokens, float* grad_
                       reinterpret_cast<unsigned*>(ws + p.off_k1)};
     int* v[2] = {reinterpret_cast<int*>(ws + p.off_v0), reinterpret_cast<int*>(ws + p.off_v1)};
     int* hist = reinterpret_cast<int*>(ws + p.off_hist);
+    int* total = reinterpret_cast<int*>(ws + p.off_total);
     const int n = batch_seq;
 
-    hipLaunchKernelGGL(prep_keys_kernel, dim3((n + 255) / 256), dim3(256), 0, st, tokens, k[0],
-                       v[0], n, vocab);
     int cur = 0;
     for (int pass = 0; pass < p.passes; ++pass) {
         const int shift = 8 * pass;
-        hipLaunchKernelGGL(radix_hist_kernel, dim3(p.ntiles), dim3(256), 0, st, k[cur], n, shift,
-                           p.ntiles, hist);
-        hipLaunchKernelGGL(exclusive_scan_kernel, dim3(1), dim3(1024), 0, st, hist,
-                           p.ntiles * kDigits);
+        const int* ids = pass == 0 ? tokens : nullptr;  // pass 0 keys come from the ids
+        hipLaunchKernelGGL(radix_hist_kernel, dim3(p.ntiles), dim3(kTile), 0, st, k[cur], ids,
+                           vocab, n, shift, p.ntiles, hist);
+        hipLaunchKernelGGL(digit_scan_kernel, dim3(kDigits), dim3(256), 0, st, hist, total,
+                           p.ntiles);
         hipLaunchKernelGGL(radix_scatter_kernel, dim3(p.ntiles), dim3(kWave), 0, st, k[cur],
-                           v[cur], k[cur ^ 1], v[cur ^ 1], n, shift, p.ntiles, hist);
+                           v[cur], ids, vocab, k[cur ^ 1], v[cur ^ 1], n, shift, p.ntiles, hist,
+                           total);
         cur ^= 1;
     }
     const dim3 grid((n + kRowWaves - 1) / kRowWaves), block(kRowWaves * kWave);

@@ -449,12 +449,13 @@ BwdPlan plan_bwd(int rows, int cols, bool vec4) {
     BwdPlan p;
     p.W = vec4 ? 4 : 1;
     const int nv = cols / p.W;
-    // (G, largest N) pairs keep the combine LDS at or under 48 KB:
-    // G = 1: 4 slots of 2*N*W*64 floats; G = 4: 1 slot of 2*N*W*256 floats;
-    // G = 8: one group per workgroup, no combine.
+    // N <= 6 keeps the combine LDS at or under 48 KB (G = 1: 4 slots of
+    // 2*N*W*64 floats; G = 4: 1 slot of 2*N*W*256 floats; G = 8: one group
+    // per workgroup, no combine) and the registers within budget (N = 8 with
+    // W = 4 spills).  Wider rows use the block-per-row kernel.
     static const int kG[] = {1, 4, 8};
-    static const int kMaxN[] = {6, 6, 8};
-    static const int kN[] = {1, 2, 3, 4, 6, 8};
+    static const int kMaxN[] = {6, 6, 6};
+    static const int kN[] = {1, 2, 3, 4, 6};
     for (int gi = 0; gi < 3 && !p.N; ++gi) {
         const int g = kG[gi];
         const int need = (nv + g * kWave - 1) / (g * kWave);
@@ -496,7 +497,6 @@ void dispatch_bwd_n(const BwdPlan& p, hipStream_t st, const float* g, const floa
         case 3: launch_bwd_group<W, 3, G, ADD>(p, st, g, x, m, s, gamma, gx, part, rows, cols); break;
         case 4: launch_bwd_group<W, 4, G, ADD>(p, st, g, x, m, s, gamma, gx, part, rows, cols); break;
         case 6: launch_bwd_group<W, 6, G, ADD>(p, st, g, x, m, s, gamma, gx, part, rows, cols); break;
-        case 8: launch_bwd_group<W, 8, G, ADD>(p, st, g, x, m, s, gamma, gx, part, rows, cols); break;
         default: break;
     }
 }
