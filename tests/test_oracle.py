@@ -392,3 +392,25 @@ def test_planted_mistake_in_gelu_derivative_is_caught():
     # missing the factor 3 in the cubic term's derivative
     wrong = 0.5 * (1 + t) + 0.5 * u * (1 - t * t) * k0 * (1 + 0.044715 * u * u)
     assert not np.allclose(d["g"] * wrong, d["gin"], rtol=1e-4, atol=1e-6)
+
+
+def test_embedding_backwards_are_adjoints_of_the_forwards():
+    # <fwd(p), g> = <p, bwd(g)> for the linear maps p -> embedding_forward(p)
+    # and p -> pos_embedding_forward(p, 0); the forwards are pinned bit-exact
+    # against the reference's CPU routines above, so this pins the backwards
+    # independently of their own loops.
+    r = rng(13)
+    V, D, B, T = 50, 24, 3, 7
+    tokens = r.integers(0, V, B * T).astype(np.int32)
+    table = r.standard_normal((V, D)).astype(np.float32)
+    pos = r.standard_normal((T, D)).astype(np.float32)
+    g = r.standard_normal((B * T, D)).astype(np.float32)
+    lhs = float((O.embedding_forward(table, tokens).astype(np.float64) * g).sum())
+    rhs = float((table.astype(np.float64)
+                 * O.embedding_backward(g, tokens, np.zeros((V, D), np.float32))).sum())
+    assert abs(lhs - rhs) <= 1e-4 * (abs(lhs) + 1)
+    zeros = np.zeros((B * T, D), np.float32)
+    lhs = float((O.pos_embedding_forward(pos, zeros, B, T).astype(np.float64) * g).sum())
+    rhs = float((pos.astype(np.float64)
+                 * O.pos_embedding_backward(g, np.zeros((T, D), np.float32), B, T)).sum())
+    assert abs(lhs - rhs) <= 1e-4 * (abs(lhs) + 1)
