@@ -37,7 +37,7 @@ namespace {
 
 constexpr int kThreads = 256;
 #ifndef MI_EW_UNROLL
-#define MI_EW_UNROLL 4
+#define MI_EW_UNROLL 1
 #endif
 #ifndef MI_FWD_BANDS
 #define MI_FWD_BANDS 512
@@ -150,25 +150,31 @@ int launch_flat(const char* name, Op op, long long nvec, hipStream_t st) {
 // ---------------------------------------------------------------------------
 // Row-band broadcast kernels.  An Op provides
 //   In load(size_t vec_index) const;          // HBM loads of one vector
-//   fvec<W> apply(size_t vec_index, const In&, const fvec<W>& bias) const;
-// apply() writes the output vector (if any) and returns the vector that
-// contributes to the column sum (ignored by the non-reducing kernel).
+//   fvec<W> apply(size_t vec_index, const In&, const fvec<W>& bias,
+//                 bool store = true) const;
+// apply() writes the output vector (if any, and if `store`) and returns the
+// vector that contributes to the column sum (ignored by the non-reducing
+// kernel).
 //
 // A workgroup of T threads covers whole rows: thread t owns the column
 // vectors j = t + k*T, k < NC, and keeps their bias vectors and column sums
 // in registers.  Workgroup b handles rows b, b + G, b + 2G, ... (G = grid
 // size), so at any moment the resident workgroups stream one contiguous band
-// of rows and HBM sees a linear sweep.  Rows are processed in batches of
-// kUnroll, with the next batch's loads issued before the current batch is
-// computed (software pipeline).  Rows wider than 4 x 1024 vectors use the
-// column-slice fallback below.
+// of rows and HBM sees a linear sweep.  Rows are processed in batches of U
+// (default 1): the batch's loads are issued together, then the batch is
+// computed and stored.  On the [8192, 3072] GELU backward, one row per batch
+// measured 49.5 us against 50.8 / 53.5 / 54.1 us for 2 / 3 / 4 rows, and
+// keeping a second batch in flight during the computation was about 3 us
+// slower still.  Rows wider than 4 x 1024 vectors use the column-slice
+// fallback below.
 // ---------------------------------------------------------------------------
 template <int W, int NC, class Op, bool REDUCE>
 __global__ __launch_bounds__(1024) void rowband_kernel(Op op, const float* __restrict__ bias,
                                                        float* __restrict__ part, int rows, int nv) {
-    // Pipeline depth shrinks as the per-thread width grows, so the buffers
-    // stay within the 128 VGPRs a 1024-thread workgroup allows (no spills).
-    constexpr int U = NC == 1 ? kUnroll : (NC == 2 ? 2 : 1);
+    // Rows per batch (MI_EW_UNROLL, default 1); widths of 3+ vectors per
+    // thread use single rows to stay within the 128 VGPRs a 1024-thread
+    // workgroup allows (no spills).
+    constexpr int U = NC <= 2 ? kUnroll : 1;
     const int T = blockDim.x;
     const int G = gridDim.x;
     fvec<W> bv[NC], acc[NC];
@@ -178,54 +184,57 @@ __global__ __launch_bounds__(1024) void rowband_kernel(Op op, const float* __res
         bv[k] = (bias && j < nv) ? vload<W>(bias, j) : vzero<W>();
         acc[k] = vzero<W>();
     }
-    typename Op::In cur[U][NC], nxt[U][NC];
-    auto load_batch = [&](int r, typename Op::In (&d)[U][NC]) {
+    // Loads are unconditional: row and column indices are clamped into the
+    // tensor and the results of clamped slots are discarded, so the loads
+    // carry no branches and the compiler waits for each row just before it
+    // is used.
+    using In = typename Op::In;
+    auto load_batch = [&](int r, In (&d)[U][NC]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int row = r + u * G;
-            if (row < rows) {
+            const int rr = row < rows ? row : rows - 1;
 #pragma unroll
-                for (int k = 0; k < NC; ++k) {
-                    const int j = threadIdx.x + k * T;
-                    if (j < nv) d[u][k] = op.load(static_cast<size_t>(row) * nv + j);
+            for (int k = 0; k < NC; ++k) {
+                const int j = threadIdx.x + k * T;
+                const int jj = j < nv ? j : nv - 1;
+                d[u][k] = op.load(static_cast<size_t>(rr) * nv + jj);
+            }
+        }
+    };
+    // Clamped slots compute a discarded value; only the store and the
+    // column-sum update are predicated.  The batch's inputs are consumed
+    // unconditionally before the first store, so no load is sunk into a
+    // predicated store and no wait has to cover a store.
+    auto run_batch = [&](int r, const In (&d)[U][NC]) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int k = 0; k < NC; ++k) d[u][k].consume();
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int row = r + u * G;
+            const bool row_ok = row < rows;
+            const size_t rb = static_cast<size_t>(row_ok ? row : 0) * nv;
+#pragma unroll
+            for (int k = 0; k < NC; ++k) {
+                const int j = threadIdx.x + k * T;
+                const bool ok = row_ok && j < nv;
+                const fvec<W> c = op.apply(rb + (j < nv ? j : 0), d[u][k], bv[k], ok);
+                if constexpr (REDUCE) {
+#pragma unroll
+                    for (int e = 0; e < W; ++e) acc[k].v[e] += ok ? c.v[e] : 0.0f;
                 }
             }
         }
     };
-    // Widths of 3+ vectors per thread already keep several loads in flight;
-    // they skip the prefetch buffer to stay spill-free.
-    constexpr bool kPrefetch = NC <= 2;
     const int step = U * G;
-    int r = blockIdx.x;
-    load_batch(r, cur);
-    for (; r < rows; r += step) {
-        if (kPrefetch && r + step < rows) load_batch(r + step, nxt);
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int row = r + u * G;
-            if (row < rows) {
-#pragma unroll
-                for (int k = 0; k < NC; ++k) {
-                    const int j = threadIdx.x + k * T;
-                    if (j < nv) {
-                        const fvec<W> c =
-                            op.apply(static_cast<size_t>(row) * nv + j, cur[u][k], bv[k]);
-                        if constexpr (REDUCE) {
-#pragma unroll
-                            for (int e = 0; e < W; ++e) acc[k].v[e] += c.v[e];
-                        }
-                    }
-                }
-            }
-        }
-        if constexpr (kPrefetch) {
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-#pragma unroll
-                for (int k = 0; k < NC; ++k) cur[u][k] = nxt[u][k];
-        } else if (r + step < rows) {
-            load_batch(r + step, cur);
-        }
+    const int first = blockIdx.x;
+    const int iters = first < rows ? (rows - first + step - 1) / step : 0;
+    In A[U][NC];
+    for (int i = 0, r = first; i < iters; ++i, r += step) {
+        load_batch(r, A);
+        run_batch(r, A);
     }
     if constexpr (REDUCE) {
         float* prow = part + static_cast<size_t>(blockIdx.x) * nv * W;
@@ -244,13 +253,17 @@ struct ResidBiasOp {  // out = (a + x) + bias
     float* out;
     struct In {
         fvec<W> a, x;
+        __device__ void consume() const {
+            mi::consume(a);
+            mi::consume(x);
+        }
     };
     __device__ In load(size_t i) const { return {sload<W>(a, i), sload<W>(x, i)}; }
-    __device__ fvec<W> apply(size_t i, const In& in, const fvec<W>& b) const {
+    __device__ fvec<W> apply(size_t i, const In& in, const fvec<W>& b, bool store = true) const {
         fvec<W> o;
 #pragma unroll
         for (int e = 0; e < W; ++e) o.v[e] = in.a.v[e] + in.x.v[e] + b.v[e];
-        sstore<W>(out, i, o);
+        if (store) sstore<W>(out, i, o);
         return o;
     }
 };
@@ -260,13 +273,14 @@ struct BiasAddOp {  // out += bias (in place)
     float* out;
     struct In {
         fvec<W> o;
+        __device__ void consume() const { mi::consume(o); }
     };
     __device__ In load(size_t i) const { return {sload<W>(out, i)}; }
-    __device__ fvec<W> apply(size_t i, const In& in, const fvec<W>& b) const {
+    __device__ fvec<W> apply(size_t i, const In& in, const fvec<W>& b, bool store = true) const {
         fvec<W> o;
 #pragma unroll
         for (int e = 0; e < W; ++e) o.v[e] = in.o.v[e] + b.v[e];
-        sstore<W>(out, i, o);
+        if (store) sstore<W>(out, i, o);
         return o;
     }
 };
@@ -277,16 +291,17 @@ struct BiasReluOp {  // out = max(in + bias, 0)
     float* out;
     struct In {
         fvec<W> x;
+        __device__ void consume() const { mi::consume(x); }
     };
     __device__ In load(size_t i) const { return {sload<W>(in, i)}; }
-    __device__ fvec<W> apply(size_t i, const In& v, const fvec<W>& b) const {
+    __device__ fvec<W> apply(size_t i, const In& v, const fvec<W>& b, bool store = true) const {
         fvec<W> o;
 #pragma unroll
         for (int e = 0; e < W; ++e) {
             const float t = v.x.v[e] + b.v[e];
             o.v[e] = (t > 0.0f) ? t : 0.0f;
         }
-        sstore<W>(out, i, o);
+        if (store) sstore<W>(out, i, o);
         return o;
     }
 };
@@ -297,13 +312,14 @@ struct BiasGeluOp {  // out = gelu(in + bias)
     float* out;
     struct In {
         fvec<W> x;
+        __device__ void consume() const { mi::consume(x); }
     };
     __device__ In load(size_t i) const { return {sload<W>(in, i)}; }
-    __device__ fvec<W> apply(size_t i, const In& v, const fvec<W>& b) const {
+    __device__ fvec<W> apply(size_t i, const In& v, const fvec<W>& b, bool store = true) const {
         fvec<W> o;
 #pragma unroll
         for (int e = 0; e < W; ++e) o.v[e] = gelu_fwd(v.x.v[e] + b.v[e]);
-        sstore<W>(out, i, o);
+        if (store) sstore<W>(out, i, o);
         return o;
     }
 };
@@ -313,9 +329,12 @@ struct ColSumOp {  // dbias partials of grad
     const float* g;
     struct In {
         fvec<W> g;
+        __device__ void consume() const { mi::consume(g); }
     };
     __device__ In load(size_t i) const { return {sload<W>(g, i)}; }
-    __device__ fvec<W> apply(size_t, const In& v, const fvec<W>&) const { return v.g; }
+    __device__ fvec<W> apply(size_t, const In& v, const fvec<W>&, bool = true) const {
+        return v.g;
+    }
 };
 
 template <int W>
@@ -325,13 +344,17 @@ struct ReluBwdBiasOp {  // gin = mask > 0 ? g : 0
     float* gin;
     struct In {
         fvec<W> m, g;
+        __device__ void consume() const {
+            mi::consume(m);
+            mi::consume(g);
+        }
     };
     __device__ In load(size_t i) const { return {sload<W>(mask, i), sload<W>(g, i)}; }
-    __device__ fvec<W> apply(size_t i, const In& v, const fvec<W>&) const {
+    __device__ fvec<W> apply(size_t i, const In& v, const fvec<W>&, bool store = true) const {
         fvec<W> o;
 #pragma unroll
         for (int e = 0; e < W; ++e) o.v[e] = (v.m.v[e] > 0.0f) ? v.g.v[e] : 0.0f;
-        sstore<W>(gin, i, o);
+        if (store) sstore<W>(gin, i, o);
         return o;
     }
 };
@@ -343,13 +366,17 @@ struct GeluBwdBiasOp {  // gin = g * gelu'(in + bias)
     float* gin;
     struct In {
         fvec<W> x, g;
+        __device__ void consume() const {
+            mi::consume(x);
+            mi::consume(g);
+        }
     };
     __device__ In load(size_t i) const { return {sload<W>(in, i), sload<W>(g, i)}; }
-    __device__ fvec<W> apply(size_t i, const In& v, const fvec<W>& b) const {
+    __device__ fvec<W> apply(size_t i, const In& v, const fvec<W>& b, bool store = true) const {
         fvec<W> o;
 #pragma unroll
         for (int e = 0; e < W; ++e) o.v[e] = v.g.v[e] * gelu_grad(v.x.v[e] + b.v[e]);
-        sstore<W>(gin, i, o);
+        if (store) sstore<W>(gin, i, o);
         return o;
     }
 };

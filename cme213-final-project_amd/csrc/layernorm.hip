@@ -191,56 +191,57 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void ln_bwd_group_kernel(
     }
 
     const int stride = gridDim.x * GPB;
-    // One row's inputs; the next row's are loaded before the current row is
-    // processed (software pipeline), so loads stay in flight during the
-    // reductions and the dx stores.
+    // One row's inputs.  Every load is unconditional (row and column indices
+    // are clamped into the tensor, masked slots are zeroed after the load),
+    // so the loads carry no branches.  Loading the next row while the
+    // current one is processed measured 0.5 us slower at [8192, 768].
     struct RowIn {
         fvec<W> go[N], xv[N];
         float mu, is;
     };
     auto load_row = [&](int row, RowIn& d) {
-        const bool valid = row < rows;
-        const size_t off = static_cast<size_t>(valid ? row : 0) * cols;
+        const int rr = row < rows ? row : rows - 1;
+        const size_t off = static_cast<size_t>(rr) * cols;
 #pragma unroll
         for (int k = 0; k < N; ++k) {
             const int j = t + k * GT;
-            const bool ok = valid && j < nv;
-            d.go[k] = ok ? sload<W>(gout + off, j) : vzero<W>();
-            d.xv[k] = ok ? sload<W>(x + off, j) : vzero<W>();
+            const int jj = j < nv ? j : nv - 1;
+            d.go[k] = sload<W>(gout + off, jj);
+            d.xv[k] = sload<W>(x + off, jj);
         }
-        d.mu = valid ? mean[row] : 0.0f;
-        d.is = valid ? rstd[row] : 0.0f;
+        d.mu = mean[rr];
+        d.is = rstd[rr];
     };
-    RowIn cur, nxt;
-    int base_row = blockIdx.x * GPB;
-    load_row(base_row + grp, cur);
-    int it = 0;
-    // The trip count is uniform across the workgroup (groups past the last
-    // row idle through the iteration) so the barriers below are reached by
-    // every wave.
-    for (; base_row < rows; base_row += stride, ++it) {
-        const int row = base_row + grp;
+    auto process = [&](const RowIn& cur, int row, int parity) {
         const bool valid = row < rows;
         const size_t off = static_cast<size_t>(valid ? row : 0) * cols;
-        if (base_row + stride < rows) load_row(base_row + stride + grp, nxt);
         const float mu = cur.mu;
         const float is = cur.is;
-
+        // Masked slots (past the row end, or a group with no row) get
+        // go = 0, so they add exact zeros to every sum.
+        fvec<W> go[N];
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            const bool ok = valid && (t + k * GT) < nv;
+#pragma unroll
+            for (int e = 0; e < W; ++e) go[k].v[e] = ok ? cur.go[k].v[e] : 0.0f;
+        }
         float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
         for (int k = 0; k < N; ++k)
 #pragma unroll
             for (int e = 0; e < W; ++e) {
                 const float xh = (cur.xv[k].v[e] - mu) * is;
-                const float dh = cur.go[k].v[e] * gm[k].v[e];
+                const float dh = go[k].v[e] * gm[k].v[e];
                 s1 += dh;
                 s2 += dh * xh;
             }
-        // Masked slots hold go = 0, so they add exact zeros to s1 and s2.
         float S1 = wave_sum(s1);
         float S2 = wave_sum(s2);
         if constexpr (G > 1) {
-            float(*r)[2] = red[it & 1];
+            // red alternates with the row parity, so the next row's writes
+            // cannot race these reads.
+            float(*r)[2] = red[parity];
             if (lane == 0) {
                 r[wave][0] = S1;
                 r[wave][1] = S2;
@@ -254,12 +255,19 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void ln_bwd_group_kernel(
                 S1 += r[w0 + i][0];
                 S2 += r[w0 + i][1];
             }
-            // red is double-buffered by iteration parity, so the next
-            // iteration's writes cannot race these reads.
         }
         const float m1 = S1 / static_cast<float>(cols);
         const float m2 = S2 / static_cast<float>(cols);
 
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+#pragma unroll
+            for (int e = 0; e < W; ++e) {
+                const float xh = (cur.xv[k].v[e] - mu) * is;
+                ag[k].v[e] += go[k].v[e] * xh;
+                ab[k].v[e] += go[k].v[e];
+            }
+        }
         if (valid) {
 #pragma unroll
             for (int k = 0; k < N; ++k) {
@@ -269,22 +277,29 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void ln_bwd_group_kernel(
                     if constexpr (ADD) d = sload<W>(gx + off, j);
 #pragma unroll
                     for (int e = 0; e < W; ++e) {
-                        const float go = cur.go[k].v[e];
                         const float xh = (cur.xv[k].v[e] - mu) * is;
-                        const float dh = go * gm[k].v[e];
+                        const float dh = go[k].v[e] * gm[k].v[e];
                         const float dx = is * (dh - m1 - xh * m2);
                         if constexpr (ADD)
-                            d.v[e] = d.v[e] + dx;
+                            d.v[e] = d.v[e] + rounded(dx);
                         else
                             d.v[e] = dx;
-                        ag[k].v[e] += go * xh;
-                        ab[k].v[e] += go;
                     }
                     sstore<W>(gx + off, j, d);
                 }
             }
         }
-        cur = nxt;
+    };
+
+    // The trip count is uniform across the workgroup (groups past the last
+    // row process a masked row), so the barriers in process() are reached by
+    // every wave.
+    const int first = blockIdx.x * GPB;
+    const int iters = first < rows ? (rows - first + stride - 1) / stride : 0;
+    RowIn cur;
+    for (int i = 0, row = first + grp; i < iters; ++i, row += stride) {
+        load_row(row, cur);
+        process(cur, row, i & 1);
     }
 
     // Combine the GPB groups' running sums: a fixed binary tree through LDS.
@@ -363,7 +378,7 @@ __global__ __launch_bounds__(kBlockThreads) void ln_bwd_block_kernel(
             const float dh = g * gamma[c];
             const float dx = is * (dh - m1 - xh * m2);
             if constexpr (ADD)
-                gx[off + c] = gx[off + c] + dx;
+                gx[off + c] = gx[off + c] + rounded(dx);
             else
                 gx[off + c] = dx;
             pg[c] = pg[c] + g * xh;

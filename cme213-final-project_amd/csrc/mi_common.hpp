@@ -98,6 +98,25 @@ __device__ __forceinline__ float readlane(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+// Returns v unchanged but hides how it was computed, so that an add which
+// consumes it is rounded on its own instead of being contracted into an FMA
+// with the multiply that produced v.  Fused "out += f(...)" paths use it to
+// give the same bits as computing f and then adding.
+__device__ __forceinline__ float rounded(float v) {
+    asm("" : "+v"(v));
+    return v;
+}
+
+// Marks a loaded vector as used at this point, unconditionally.  Without it
+// the compiler may sink a load whose only uses sit under a predicated store
+// into that branch, which serialises the loads of a batch and adds full
+// memory-queue waits.
+template <int W>
+__device__ __forceinline__ void consume(const fvec<W>& x) {
+#pragma unroll
+    for (int e = 0; e < W; ++e) asm volatile("" ::"v"(x.v[e]));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
     v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
     v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2

@@ -38,6 +38,14 @@ __global__ __launch_bounds__(kFinThreads) void colsum_finalize_kernel(
     const int c = blockIdx.x * kFinCols + cl;
     const int p0 = static_cast<int>(static_cast<long long>(slice) * P / kFinSlices);
     const int p1 = static_cast<int>(static_cast<long long>(slice + 1) * P / kFinSlices);
+    // The accumulated output's old value is loaded first, so its round trip
+    // overlaps the partial-row loads instead of following the LDS combine.
+    float* o = nullptr;
+    float old = 0.0f;
+    if (slice == 0 && c < ncols) {
+        o = (c < split) ? (out0 + c) : (out1 + (c - split));
+        old = *o;
+    }
     // All loads of a chunk are issued before the first add, so a thread waits
     // for one memory round trip per kChunk partial rows.
     float s = 0.0f;
@@ -59,8 +67,7 @@ __global__ __launch_bounds__(kFinThreads) void colsum_finalize_kernel(
         float t = tot[0][cl];
 #pragma unroll
         for (int w = 1; w < kFinSlices; ++w) t += tot[w][cl];
-        float* o = (c < split) ? (out0 + c) : (out1 + (c - split));
-        *o = *o + t;
+        *o = old + t;
     }
 }
 
