@@ -39,6 +39,9 @@ constexpr int kThreads = 256;
 #ifndef MI_EW_UNROLL
 #define MI_EW_UNROLL 1
 #endif
+#ifndef MI_FLAT_MAX_GRID
+#define MI_FLAT_MAX_GRID 16384
+#endif
 #ifndef MI_FWD_BANDS
 #define MI_FWD_BANDS 512
 #endif
@@ -510,7 +513,7 @@ int launch_rowtile(const char* name, Op op, const float* bias, int rows, int col
     const unsigned long long nvec = static_cast<unsigned long long>(rows) * nv;
     if (MI_FWD_FLAT && nvec < (1ull << 32)) {
         long long grid = (static_cast<long long>(nvec) + kThreads - 1) / kThreads;
-        if (grid > 16384) grid = 16384;
+        if (grid > MI_FLAT_MAX_GRID) grid = MI_FLAT_MAX_GRID;
         hipLaunchKernelGGL((flatbias_kernel<W, Op>), dim3(static_cast<unsigned>(grid)),
                            dim3(kThreads), 0, st, op, bias, static_cast<unsigned>(nvec),
                            make_udiv(static_cast<unsigned>(nv)));

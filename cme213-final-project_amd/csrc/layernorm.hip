@@ -38,72 +38,96 @@ constexpr int kBwdWaves = MI_LN_BWD_WAVES;  // waves per backward workgroup
 constexpr int kBlockThreads = 256;  // generic block-per-row kernels
 
 // ---------------------------------------------------------------------------
-// Forward, one wave per row.
+// Forward: each wave normalises kFwdRows consecutive rows, held in registers.
+// All loads of those rows are issued first (column indices clamped into the
+// row, masked slots zeroed afterwards), then each row is reduced and written.
 // ---------------------------------------------------------------------------
+#ifndef MI_LN_FWD_ROWS
+#define MI_LN_FWD_ROWS 2
+#endif
+constexpr int kFwdRows = MI_LN_FWD_ROWS;
+
 template <int W, int N, bool SAVE, bool RESID>
 __global__ __launch_bounds__(kFwdWaves * kWave) void ln_fwd_wave_kernel(
     const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ gamma,
     const float* __restrict__ beta, float* __restrict__ resid_out, float* __restrict__ out,
     float* __restrict__ mean_out, float* __restrict__ rstd_out, int rows, int cols, float eps) {
     const int lane = threadIdx.x & (kWave - 1);
-    const int row = blockIdx.x * kFwdWaves + static_cast<int>(threadIdx.x / kWave);
-    if (row >= rows) return;  // wave-uniform
+    const int row0 = (blockIdx.x * kFwdWaves + static_cast<int>(threadIdx.x / kWave)) * kFwdRows;
+    if (row0 >= rows) return;  // wave-uniform
     const int nv = cols / W;
-    const size_t base = static_cast<size_t>(row) * cols;
 
-    fvec<W> v[N];
+    fvec<W> v[kFwdRows][N];
 #pragma unroll
-    for (int k = 0; k < N; ++k) {
-        const int j = lane + k * kWave;
-        if (j < nv) {
-            v[k] = sload<W>(a + base, j);
+    for (int r = 0; r < kFwdRows; ++r) {
+        const int rr = row0 + r < rows ? row0 + r : rows - 1;
+        const size_t base = static_cast<size_t>(rr) * cols;
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            const int j = lane + k * kWave;
+            const int jj = j < nv ? j : nv - 1;
+            v[r][k] = sload<W>(a + base, jj);
             if constexpr (RESID) {
-                const fvec<W> w = sload<W>(b + base, j);
+                const fvec<W> w = sload<W>(b + base, jj);
 #pragma unroll
-                for (int e = 0; e < W; ++e) v[k].v[e] = v[k].v[e] + w.v[e];
-                sstore<W>(resid_out + base, j, v[k]);
+                for (int e = 0; e < W; ++e) v[r][k].v[e] = v[r][k].v[e] + w.v[e];
             }
-        } else {
-            v[k] = vzero<W>();
-        }
-    }
-
-    float s = 0.0f;
-#pragma unroll
-    for (int k = 0; k < N; ++k)
-#pragma unroll
-        for (int e = 0; e < W; ++e) s += v[k].v[e];
-    const float mean = wave_sum(s) / static_cast<float>(cols);
-
-    float q = 0.0f;
-#pragma unroll
-    for (int k = 0; k < N; ++k) {
-        const bool ok = (lane + k * kWave) < nv;
-#pragma unroll
-        for (int e = 0; e < W; ++e) {
-            const float d = ok ? (v[k].v[e] - mean) : 0.0f;
-            q += d * d;
-        }
-    }
-    const float var = wave_sum(q) / static_cast<float>(cols);
-    const float rstd = 1.0f / sqrtf(var + eps);
-    if constexpr (SAVE) {
-        if (lane == 0) {
-            mean_out[row] = mean;
-            rstd_out[row] = rstd;
         }
     }
 
 #pragma unroll
-    for (int k = 0; k < N; ++k) {
-        const int j = lane + k * kWave;
-        if (j < nv) {
-            const fvec<W> g = vload<W>(gamma, j);
-            const fvec<W> bt = vload<W>(beta, j);
-            fvec<W> y;
+    for (int r = 0; r < kFwdRows; ++r) {
+        const int row = row0 + r;
+        if (row >= rows) break;  // wave-uniform
+        const size_t base = static_cast<size_t>(row) * cols;
 #pragma unroll
-            for (int e = 0; e < W; ++e) y.v[e] = (v[k].v[e] - mean) * rstd * g.v[e] + bt.v[e];
-            sstore<W>(out + base, j, y);
+        for (int k = 0; k < N; ++k) {
+            const bool ok = (lane + k * kWave) < nv;
+            if constexpr (RESID) {
+                if (ok) sstore<W>(resid_out + base, lane + k * kWave, v[r][k]);
+            }
+#pragma unroll
+            for (int e = 0; e < W; ++e) v[r][k].v[e] = ok ? v[r][k].v[e] : 0.0f;
+        }
+
+        float s = 0.0f;
+#pragma unroll
+        for (int k = 0; k < N; ++k)
+#pragma unroll
+            for (int e = 0; e < W; ++e) s += v[r][k].v[e];
+        const float mean = wave_sum(s) / static_cast<float>(cols);
+
+        float q = 0.0f;
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            const bool ok = (lane + k * kWave) < nv;
+#pragma unroll
+            for (int e = 0; e < W; ++e) {
+                const float d = ok ? (v[r][k].v[e] - mean) : 0.0f;
+                q += d * d;
+            }
+        }
+        const float var = wave_sum(q) / static_cast<float>(cols);
+        const float rstd = 1.0f / sqrtf(var + eps);
+        if constexpr (SAVE) {
+            if (lane == 0) {
+                mean_out[row] = mean;
+                rstd_out[row] = rstd;
+            }
+        }
+
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            const int j = lane + k * kWave;
+            if (j < nv) {
+                const fvec<W> g = vload<W>(gamma, j);
+                const fvec<W> bt = vload<W>(beta, j);
+                fvec<W> y;
+#pragma unroll
+                for (int e = 0; e < W; ++e)
+                    y.v[e] = (v[r][k].v[e] - mean) * rstd * g.v[e] + bt.v[e];
+                sstore<W>(out + base, j, y);
+            }
         }
     }
 }
@@ -440,7 +464,8 @@ int ln_forward_impl(const char* name, const float* a, const float* b, const floa
     const int need = (cols / W + kWave - 1) / kWave;
     const int n = pick_n(need);
     if (n != 0) {
-        const dim3 grid((rows + kFwdWaves - 1) / kFwdWaves);
+        const int waves = (rows + kFwdRows - 1) / kFwdRows;
+        const dim3 grid((waves + kFwdWaves - 1) / kFwdWaves);
         if (vec4)
             launch_fwd_wave<4, SAVE, RESID>(n, grid, st, a, b, gamma, beta, ro, out, mo, so, rows,
                                             cols, eps);
