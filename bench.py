@@ -23,7 +23,8 @@ Also reported on the same line:
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 --workload picks another BASELINE config (ln, gelu, embedding, block12, xl48,
-wide); the default is the headline metric.
+wide) or the softmax cross-entropy of the model loss (ce); the default is the
+headline metric.
 """
 import argparse
 import json
@@ -76,11 +77,12 @@ WORKLOADS = {
     "block12": "config 3: GPT-2-small non-GEMM block x12 layers, [8192,768] / [8192,3072]",
     "xl48": "config 4: GPT-2-XL-shaped non-GEMM block x48 layers, [4096,1600] / [4096,6400]",
     "wide": "config 4 wide sweep: LN fwd+bwd [32768,4096]",
+    "ce": "softmax cross-entropy of the model loss: logits [8192,50257] (B=8, T=1024, GPT-2 vocab)",
 }
 
 
 def make_workload(name):
-    from cme213_amd.workloads import BlockSequence, Embedding, FwdBwd, Headline
+    from cme213_amd.workloads import BlockSequence, CrossEntropy, Embedding, FwdBwd, Headline
     if name == "headline":
         return Headline()
     if name == "ln":
@@ -95,6 +97,8 @@ def make_workload(name):
         return BlockSequence(4096, 1600, 6400, 48)
     if name == "wide":
         return FwdBwd(32768, 4096, 0, gelu=False)
+    if name == "ce":
+        return CrossEntropy()
     raise SystemExit(f"unknown workload {name}; choose from {sorted(WORKLOADS)}")
 
 

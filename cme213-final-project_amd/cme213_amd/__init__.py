@@ -98,6 +98,11 @@ _SIGS = {
     "mi_pos_embedding_forward": (c_int, [P, P, c_int, c_int, c_int, P]),
     "mi_pos_embedding_backward": (c_int, [P, P, c_int, c_int, c_int, P]),
     "mi_embedding_pos_forward": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, P]),
+    # softmax / cross-entropy
+    "mi_softmax_forward": (c_int, [P, P, c_int, c_int, P]),
+    "mi_cross_entropy_forward": (c_int, [P, P, P, c_int, c_int, P, P]),
+    "mi_cross_entropy_forward_v2": (c_int, [P, P, P, P, P, c_int, c_int, P]),
+    "mi_cross_entropy_workspace": (c_size_t, [c_int]),
 }
 
 for _name, (_res, _args) in _SIGS.items():
@@ -276,3 +281,21 @@ def pos_embedding_backward(grad_out, grad_pos_table, batch, seq, dim, stream=Non
 def embedding_pos_forward(table, pos_table, tokens, out, batch, seq, dim, vocab=0, stream=None):
     _check(lib.mi_embedding_pos_forward(_f(table), _f(pos_table), _i(tokens), _f(out), batch,
                                         seq, dim, vocab, _stream(stream)))
+
+
+def softmax_forward(x, out, rows, cols, stream=None):
+    _check(lib.mi_softmax_forward(_f(x), _f(out), rows, cols, _stream(stream)))
+
+
+def cross_entropy_forward(logits, targets, grad, batch, vocab, stream=None) -> float:
+    """Mean loss as a Python float (waits for the stream, as the reference's
+    cross_entropy_forward returns it to the host)."""
+    loss = ctypes.c_float(0.0)
+    _check(lib.mi_cross_entropy_forward(_f(logits), _i(targets), _f(grad), batch, vocab,
+                                        ctypes.byref(loss), _stream(stream)))
+    return loss.value
+
+
+def cross_entropy_forward_v2(logits, targets, grad, losses, loss_out, batch, vocab, stream=None):
+    _check(lib.mi_cross_entropy_forward_v2(_f(logits), _i(targets), _f(grad), _f(losses),
+                                           _f(loss_out), batch, vocab, _stream(stream)))

@@ -12,8 +12,8 @@ from __future__ import annotations
 
 import torch
 
-from . import (bias_gelu_forward, embedding_backward, embedding_pos_forward,
-               gelu_backward_with_bias_backward, layernorm_backward, layernorm_backward_residual,
+from . import (bias_gelu_forward, cross_entropy_forward_v2, embedding_backward,
+               embedding_pos_forward, gelu_backward_with_bias_backward, layernorm_backward, layernorm_backward_residual,
                layernorm_forward_save, pos_embedding_backward, residual_layernorm_forward_save)
 
 F32 = 4
@@ -261,6 +261,39 @@ class Embedding:
             ("emb_bwd", lambda: (embedding_backward(s["dout"], s["ids"], self.dwte, B * T, D, V),
                                  pos_embedding_backward(s["dout"], self.dwpe, B, T, D))),
         ]
+
+    def step(self, k):
+        for _, fn in self.ops(k):
+            fn()
+
+
+class CrossEntropy:
+    """Softmax cross-entropy of the reference model's loss
+    (FINAL_CLEAN_CODE/src/model/transformer.cu:402-407,
+    cross_entropy_forward_v2): logits [B*T, V] ~ N(0, 2^2), targets U[0, V).
+    Algorithmic bytes: logits read, gradient written, targets read, losses
+    written, 4(2 R V + 2 R).  `sets` logits / gradient pairs rotate."""
+
+    def __init__(self, R=8192, V=50257, sets=2, seed=20268):
+        self.R, self.V = R, V
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        self.sets = []
+        for _ in range(sets):
+            self.sets.append({
+                "logits": _randn((R, V), g, 2.0),
+                "targets": torch.randint(0, V, (R,), device="cuda", generator=g,
+                                         dtype=torch.int32),
+                "grad": torch.empty(R, V, device="cuda"),
+                "losses": torch.empty(R, device="cuda"),
+                "loss": torch.empty(1, device="cuda")})
+        self.step_bytes = F32 * (2 * R * V + 2 * R)
+        self.bytes = {"cross_entropy": self.step_bytes}
+
+    def ops(self, k):
+        s = self.sets[k % len(self.sets)]
+        return [("cross_entropy", lambda: cross_entropy_forward_v2(
+            s["logits"], s["targets"], s["grad"], s["losses"], s["loss"], self.R, self.V))]
 
     def step(self, k):
         for _, fn in self.ops(k):

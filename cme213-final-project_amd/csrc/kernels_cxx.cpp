@@ -123,3 +123,21 @@ void pos_embedding_backward(const float* grad_out, float* grad_pos_table, int ba
     MI_CHECK(mi_pos_embedding_backward(grad_out, grad_pos_table, batch, seq, dim,
                                        per_thread_stream()));
 }
+
+void softmax_forward(const float* x, float* out, int rows, int cols) {
+    MI_CHECK(mi_softmax_forward(x, out, rows, cols, per_thread_stream()));
+}
+
+float cross_entropy_forward(const float* logits, const int* targets, float* grad, int batch,
+                            int vocab) {
+    float loss = 0.0f;
+    MI_CHECK(mi_cross_entropy_forward(logits, targets, grad, batch, vocab, &loss,
+                                      per_thread_stream()));
+    return loss;
+}
+
+void cross_entropy_forward_v2(const float* logits, const int* targets, float* grad,
+                              float* d_losses, float* d_loss_out, int batch, int vocab) {
+    MI_CHECK(mi_cross_entropy_forward_v2(logits, targets, grad, d_losses, d_loss_out, batch, vocab,
+                                         per_thread_stream()));
+}

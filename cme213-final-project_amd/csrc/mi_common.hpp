@@ -129,6 +129,17 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (r0 + r1) + (r2 + r3);
 }
 
+// Wave64 maximum with the same DPP pattern; every lane returns the result.
+// (fmaxf is exact and order-independent, so only NaN handling matters: NaN
+// operands are ignored, as fmaxf ignores them.)  All 64 lanes must be active.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_move<0xB1>(v));
+    v = fmaxf(v, dpp_move<0x4E>(v));
+    v = fmaxf(v, dpp_move<0x141>(v));
+    v = fmaxf(v, dpp_move<0x140>(v));
+    return fmaxf(fmaxf(readlane(v, 0), readlane(v, 16)), fmaxf(readlane(v, 32), readlane(v, 48)));
+}
+
 // ---------------------------------------------------------------------------
 // Host plumbing (defined in runtime.hip).
 // ---------------------------------------------------------------------------

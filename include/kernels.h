@@ -17,7 +17,13 @@
 //    deterministic two-pass reduction instead of float atomics, so results
 //    are bitwise reproducible;
 //  * embedding_backward accumulates each table row in increasing token
-//    position, which makes it bit-identical to the reference's CPU loop.
+//    position, which makes it bit-identical to the reference's CPU loop;
+//  * cross_entropy_forward keeps its per-row losses in the library
+//    workspace instead of a cudaMalloc per call, and cross_entropy_forward_v2
+//    reduces the mean loss in a fixed order in one kernel (no memset, no
+//    atomics);
+//  * a cross-entropy target outside [0, vocab) gives a NaN loss instead of
+//    an out-of-bounds access.
 // The same kernels are reachable through the C ABI in mi_kernels.h.
 #pragma once
 
@@ -79,6 +85,14 @@ void bias_gelu_forward(const float* in, const float* bias, float* out,
 void gelu_backward_with_bias_backward(const float* in, const float* bias,
                                       const float* grad_out, float* grad_in,
                                       float* dbias, int rows, int cols);
+
+// --- softmax / cross-entropy (reference kernels.h:122-129) -----------------
+void softmax_forward(const float* x, float* out, int rows, int cols);
+float cross_entropy_forward(const float* logits, const int* targets,
+                            float* grad, int batch, int vocab);
+void cross_entropy_forward_v2(const float* logits, const int* targets,
+                              float* grad, float* d_losses, float* d_loss_out,
+                              int batch, int vocab);
 
 // --- embedding (reference kernels.h:131-138) -------------------------------
 void embedding_forward(const float* table, const int* tokens,

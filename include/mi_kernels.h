@@ -185,6 +185,34 @@ int mi_embedding_pos_forward(const float* table, const float* pos_table,
                              const int* tokens, float* out,
                              int batch, int seq, int dim, int vocab, void* stream);
 
+/* ----- softmax and cross-entropy ----------------------------------------- */
+
+/* out[r, :] = exp(x[r, :] - max) / sum, per row.  Replaces softmax_forward
+ * (kernels.h:122, FINAL_CLEAN_CODE/src/kernels/activations.cu:394-435). */
+int mi_softmax_forward(const float* x, float* out, int rows, int cols, void* stream);
+
+/* Softmax cross-entropy with the reference kernel's arithmetic
+ * (activations.cu:438-477): p = e * (1 / (sum + 1e-9)),
+ * loss[b] = -log(p[target] + 1e-9), grad = p - onehot(target).  Waits for
+ * the stream, copies the per-row losses back and stores their mean, summed
+ * in row order on the host, in *loss.  A target outside [0, vocab) gives a
+ * NaN loss and leaves that row's gradient at p.  Replaces
+ * cross_entropy_forward (kernels.h:124-125, activations.cu:479-499), which
+ * returns the loss; uses the library workspace for the per-row losses. */
+int mi_cross_entropy_forward(const float* logits, const int* targets, float* grad,
+                             int batch, int vocab, float* loss, void* stream);
+
+/* As above with grad scaled by 1 / batch, per-row losses in losses[batch]
+ * and their mean written to the device scalar *loss_out, summed in a fixed
+ * order (no host sync, no memset, no atomics; graph-capturable).  Replaces
+ * cross_entropy_forward_v2 (kernels.h:127-129, activations.cu:517-532). */
+int mi_cross_entropy_forward_v2(const float* logits, const int* targets, float* grad,
+                                float* losses, float* loss_out, int batch, int vocab,
+                                void* stream);
+
+/* Workspace bytes mi_cross_entropy_forward needs for `batch` rows. */
+size_t mi_cross_entropy_workspace(int batch);
+
 #ifdef __cplusplus
 }
 #endif

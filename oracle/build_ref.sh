@@ -21,6 +21,7 @@ excerpt FINAL_CLEAN_CODE/tests/test_layernorm.cu 8 24 ln_cpu.inc "static void la
 excerpt NEW_code/tests/test_embedding.cu 16 41 emb_cpu.inc "static void embedding_forward_cpu("
 excerpt FINAL_CLEAN_CODE/tests/test_fusion_benchmark.cu 8 12 fill_pattern.inc "static void fill_pattern("
 excerpt FINAL_CLEAN_CODE/tests/test_model_reference.cu 49 68 ln_f64.inc "static void layernorm("
+excerpt NEW_code/tests/test_softmax_ce.cu 26 75 softmax_ce.inc "static void softmax_cpu("
 mkdir -p "$OUT"
 g++ -std=c++17 -O2 -ffp-contract=off -fPIC -shared -I"$TMP" \
     "$HERE/ref_shim.cpp" -o "$OUT/libref_cpu.so"

@@ -445,3 +445,121 @@ void orc_pos_embedding_backward(const float* grad_out, float* grad_pos_table,
             for (int d = 0; d < dim; ++d)
                 grad_pos_table[(long)s * dim + d] += grad_out[((long)b * seq + s) * dim + d];
 }
+
+/* ----- softmax and cross-entropy ----------------------------------------- */
+
+/* Row softmax, NC/tests/test_softmax_ce.cu:26-44: max from the first
+ * element, out = expf(x - max), sequential sum, out /= sum. */
+void orc_softmax_forward(const float* x, float* out, int rows, int cols) {
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
+    for (int r = 0; r < rows; ++r) {
+        const float* row_in = x + (long)r * cols;
+        float* row_out = out + (long)r * cols;
+        float max_val = row_in[0];
+        for (int c = 1; c < cols; ++c) max_val = fmaxf(max_val, row_in[c]);
+        float sum = 0.0f;
+        for (int c = 0; c < cols; ++c) {
+            row_out[c] = expf(row_in[c] - max_val);
+            sum += row_out[c];
+        }
+        for (int c = 0; c < cols; ++c) row_out[c] /= sum;
+    }
+}
+
+/* Cross-entropy as the reference's CPU test states it,
+ * NC/tests/test_softmax_ce.cu:46-75: log-sum-exp loss, grad = softmax -
+ * onehot (unscaled); returns the mean loss (sequential float sum / batch). */
+float orc_cross_entropy_cpu(const float* logits, const int* targets, float* grad,
+                            int batch, int vocab) {
+    float total_loss = 0.0f;
+    for (int i = 0; i < batch; ++i) {
+        int target = targets[i];
+        const float* l = logits + (long)i * vocab;
+        float max_logit = l[0];
+        for (int j = 1; j < vocab; ++j) max_logit = fmaxf(max_logit, l[j]);
+        float sum_exp = 0.0f;
+        for (int j = 0; j < vocab; ++j) sum_exp += expf(l[j] - max_logit);
+        float log_sum_exp = logf(sum_exp) + max_logit;
+        float loss = log_sum_exp - l[target];
+        total_loss += loss;
+        for (int j = 0; j < vocab; ++j) {
+            float softmax_j = expf(l[j] - max_logit) / sum_exp;
+            grad[(long)i * vocab + j] = softmax_j;
+            if (j == target) grad[(long)i * vocab + j] -= 1.0f;
+        }
+    }
+    return total_loss / batch;
+}
+
+/* Cross-entropy with the arithmetic of the reference's GPU kernel
+ * (FC/src/kernels/activations.cu:438-477) and its row reductions done
+ * sequentially: e = expf(l - max) with max starting at -FLT_MAX,
+ * p = e * (1 / (sum + 1e-9)), loss = -logf(p[t] + 1e-9), grad[t] = p[t] - 1,
+ * then every grad element times scale.  A target outside [0, vocab) gives a
+ * NaN loss and no onehot term (the library's defined behaviour; the
+ * reference reads out of bounds). */
+void orc_cross_entropy_rows(const float* logits, const int* targets, float* grad,
+                            float* losses, int batch, int vocab, float scale) {
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
+    for (int b = 0; b < batch; ++b) {
+        const float* row = logits + (long)b * vocab;
+        float* g = grad + (long)b * vocab;
+        float row_max = -3.402823466e+38f;
+        for (int i = 0; i < vocab; ++i) row_max = fmaxf(row_max, row[i]);
+        float sum = 0.0f;
+        for (int i = 0; i < vocab; ++i) {
+            float e = expf(row[i] - row_max);
+            g[i] = e;
+            sum += e;
+        }
+        float inv_sum = 1.0f / (sum + 1e-9f);
+        for (int i = 0; i < vocab; ++i) g[i] *= inv_sum;
+        int tgt = targets[b];
+        if (tgt >= 0 && tgt < vocab) {
+            losses[b] = -logf(g[tgt] + 1e-9f);
+            g[tgt] -= 1.0f;
+        } else {
+            losses[b] = nanf("");
+        }
+        for (int i = 0; i < vocab; ++i) g[i] *= scale;
+    }
+}
+
+/* Mean of per-row losses summed in row order, as the host loop of
+ * cross_entropy_forward (FC/src/kernels/activations.cu:494-497). */
+float orc_loss_mean(const float* losses, int n) {
+    float total = 0.0f;
+    for (int i = 0; i < n; ++i) total += losses[i];
+    return total / n;
+}
+
+/* Double-precision cross-entropy from first principles (log-sum-exp):
+ * loss = log(sum exp(l - max)) + max - l[t], grad = softmax - onehot. */
+void orc_cross_entropy_f64(const float* logits, const int* targets, double* grad,
+                           double* losses, int batch, int vocab) {
+    for (int b = 0; b < batch; ++b) {
+        const float* row = logits + (long)b * vocab;
+        double m = row[0];
+        for (int i = 1; i < vocab; ++i) m = row[i] > m ? row[i] : m;
+        double s = 0.0;
+        for (int i = 0; i < vocab; ++i) s += exp((double)row[i] - m);
+        int t = targets[b];
+        losses[b] = log(s) + m - (double)row[t];
+        for (int i = 0; i < vocab; ++i) {
+            double p = exp((double)row[i] - m) / s;
+            grad[(long)b * vocab + i] = p - (i == t ? 1.0 : 0.0);
+        }
+    }
+}
+
+/* Double-precision softmax. */
+void orc_softmax_forward_f64(const float* x, double* out, int rows, int cols) {
+    for (int r = 0; r < rows; ++r) {
+        const float* row = x + (long)r * cols;
+        double m = row[0];
+        for (int c = 1; c < cols; ++c) m = row[c] > m ? row[c] : m;
+        double s = 0.0;
+        for (int c = 0; c < cols; ++c) s += exp((double)row[c] - m);
+        for (int c = 0; c < cols; ++c) out[(long)r * cols + c] = exp((double)row[c] - m) / s;
+    }
+}

@@ -59,11 +59,19 @@ def lib():
             "orc_embedding_backward": [P, P, P, c_int, c_int],
             "orc_pos_embedding_forward": [P, P, c_int, c_int, c_int],
             "orc_pos_embedding_backward": [P, P, c_int, c_int, c_int],
+            "orc_softmax_forward": [P, P, c_int, c_int],
+            "orc_softmax_forward_f64": [P, P, c_int, c_int],
+            "orc_cross_entropy_cpu": [P, P, P, c_int, c_int],
+            "orc_cross_entropy_rows": [P, P, P, P, c_int, c_int, c_float],
+            "orc_loss_mean": [P, c_int],
+            "orc_cross_entropy_f64": [P, P, P, P, c_int, c_int],
         }
+        restypes = {"orc_get_threads": c_int, "orc_cross_entropy_cpu": c_float,
+                    "orc_loss_mean": c_float}
         for name, args in sigs.items():
             fn = getattr(L, name)
             fn.argtypes = args
-            fn.restype = c_int if name == "orc_get_threads" else None
+            fn.restype = restypes.get(name)
         _lib = L
     return _lib
 
@@ -79,9 +87,13 @@ def ref():
         R.ref_embedding_backward_cpu.argtypes = [P, P, P, c_int, c_int, c_int]
         R.ref_pos_embedding_cpu.argtypes = [P, P, c_int, c_int, c_int]
         R.ref_fill_pattern.argtypes = [P, c_int, c_float, c_float]
+        R.ref_softmax_cpu.argtypes = [P, P, c_int, c_int]
+        R.ref_cross_entropy_cpu.argtypes = [P, P, P, c_int, c_int]
         for fn in (R.ref_layernorm_cpu, R.ref_layernorm_f64, R.ref_embedding_forward_cpu,
-                   R.ref_embedding_backward_cpu, R.ref_pos_embedding_cpu, R.ref_fill_pattern):
+                   R.ref_embedding_backward_cpu, R.ref_pos_embedding_cpu, R.ref_fill_pattern,
+                   R.ref_softmax_cpu):
             fn.restype = None
+        R.ref_cross_entropy_cpu.restype = c_float
         _ref = R
     return _ref
 
@@ -313,3 +325,56 @@ def pos_embedding_backward(g, grad_pos, batch, seq):
     gp = f32(grad_pos).copy()
     lib().orc_pos_embedding_backward(_p(g), _p(gp), batch, seq, gp.shape[1])
     return gp
+
+
+# ----- softmax / cross-entropy -----------------------------------------------
+
+def softmax_forward(x):
+    x = f32(x)
+    out = np.empty_like(x)
+    lib().orc_softmax_forward(_p(x), _p(out), x.shape[0], x.shape[1])
+    return out
+
+
+def softmax_forward_f64(x):
+    x = f32(x)
+    out = np.empty(x.shape, np.float64)
+    lib().orc_softmax_forward_f64(_p(x), _p(out), x.shape[0], x.shape[1])
+    return out
+
+
+def cross_entropy_cpu(logits, targets):
+    """NC/tests/test_softmax_ce.cu:46-75: (mean loss, unscaled grad)."""
+    logits = f32(logits)
+    targets = _c(targets, np.int32)
+    grad = np.empty_like(logits)
+    loss = lib().orc_cross_entropy_cpu(_p(logits), _p(targets), _p(grad), logits.shape[0],
+                                       logits.shape[1])
+    return float(loss), grad
+
+
+def cross_entropy_rows(logits, targets, scale=1.0):
+    """The reference GPU kernel's arithmetic (activations.cu:438-477):
+    (per-row losses, grad * scale)."""
+    logits = f32(logits)
+    targets = _c(targets, np.int32)
+    grad = np.empty_like(logits)
+    losses = np.empty(logits.shape[0], np.float32)
+    lib().orc_cross_entropy_rows(_p(logits), _p(targets), _p(grad), _p(losses), logits.shape[0],
+                                 logits.shape[1], scale)
+    return losses, grad
+
+
+def loss_mean(losses):
+    losses = f32(losses)
+    return float(lib().orc_loss_mean(_p(losses), losses.size))
+
+
+def cross_entropy_f64(logits, targets):
+    logits = f32(logits)
+    targets = _c(targets, np.int32)
+    grad = np.empty(logits.shape, np.float64)
+    losses = np.empty(logits.shape[0], np.float64)
+    lib().orc_cross_entropy_f64(_p(logits), _p(targets), _p(grad), _p(losses), logits.shape[0],
+                                logits.shape[1])
+    return losses, grad

@@ -14,6 +14,8 @@
 //                                                           pos_embedding_cpu
 //   fill_pattern.inc FC/tests/test_fusion_benchmark.cu:8-12 fill_pattern
 //   ln_f64.inc       FC/tests/test_model_reference.cu:49-68 layernorm (double)
+//   softmax_ce.inc   NC/tests/test_softmax_ce.cu:26-75      softmax_cpu,
+//                                                           cross_entropy_cpu
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
@@ -23,6 +25,7 @@
 #include "emb_cpu.inc"
 #include "fill_pattern.inc"
 #include "ln_f64.inc"
+#include "softmax_ce.inc"
 
 extern "C" {
 
@@ -58,6 +61,15 @@ void ref_fill_pattern(float* v, int n, float scale, float shift) {
     std::vector<float> tmp((size_t)n);
     fill_pattern(tmp, scale, shift);
     std::copy(tmp.begin(), tmp.end(), v);
+}
+
+void ref_softmax_cpu(const float* x, float* out, int rows, int cols) {
+    softmax_cpu(x, out, rows, cols);
+}
+
+float ref_cross_entropy_cpu(const float* logits, const int* targets, float* grad, int batch,
+                            int vocab) {
+    return cross_entropy_cpu(logits, targets, grad, batch, vocab);
 }
 
 }  // extern "C"

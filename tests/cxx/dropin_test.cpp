@@ -11,6 +11,9 @@
 //                                          bias+GELU pair
 //   NC/tests/test_embedding.cu:43-182      embedding fwd / bwd / pos fwd,
 //                                          srand(42) inputs
+//   NC/tests/test_softmax_ce.cu:77-178     softmax [256,512] and cross-entropy
+//                                          [128,4096], srand(42) inputs, the
+//                                          reference's own bounds
 // Exit status 0 = all checks passed.
 #include <hip/hip_runtime.h>
 
@@ -31,6 +34,9 @@ void orc_layernorm_forward(const float* x, const float* gamma, const float* beta
 void orc_embedding_forward(const float* table, const int* tokens, float* out, int bt, int dim);
 void orc_embedding_backward(const float* g, const int* tokens, float* gt, int bt, int dim);
 void orc_pos_embedding_forward(const float* pos, float* emb, int batch, int seq, int dim);
+void orc_softmax_forward(const float* x, float* out, int rows, int cols);
+float orc_cross_entropy_cpu(const float* logits, const int* targets, float* grad, int batch,
+                            int vocab);
 }
 
 static int g_fail = 0;
@@ -192,10 +198,51 @@ static void test_embedding() {
     check(same_bits(out.get(), ref_emb), "pos_embedding_forward == CPU (bits)", 0.0);
 }
 
+static void test_softmax_ce() {
+    std::printf("softmax / cross-entropy (NC/tests/test_softmax_ce.cu)\n");
+    {
+        const int rows = 256, cols = 512, n = rows * cols;
+        std::vector<float> hx(n), ref(n);
+        orc_srand(42);
+        orc_fill_rand_unit(hx.data(), n);
+        orc_softmax_forward(hx.data(), ref.data(), rows, cols);
+        Dev<float> x(hx), out(n);
+        softmax_forward(x.p, out.p, rows, cols);
+        const float err = max_abs_diff(out.get(), ref);
+        check(err < 1e-5f, "softmax max abs error (reference bound 1e-5)", err);
+    }
+    {
+        const int batch = 128, vocab = 4096, n = batch * vocab;
+        std::vector<float> hl(n), gref(n);
+        std::vector<int> ht(batch);
+        orc_srand(42);
+        orc_fill_rand_unit(hl.data(), n);
+        orc_fill_rand_tokens(ht.data(), batch, vocab);
+        const float loss_ref = orc_cross_entropy_cpu(hl.data(), ht.data(), gref.data(), batch, vocab);
+        Dev<float> l(hl), g(n), losses(batch), loss_out(1);
+        Dev<int> t(ht);
+        const float loss = cross_entropy_forward(l.p, t.p, g.p, batch, vocab);
+        const float grad_err = max_abs_diff(g.get(), gref);
+        const float loss_err = std::fabs(loss_ref - loss) / (std::fabs(loss_ref) + 1e-8f);
+        check(grad_err < 1e-4f, "cross-entropy grad error (reference bound 1e-4)", grad_err);
+        check(loss_err < 1e-2f, "cross-entropy loss rel error (reference bound 1e-2)", loss_err);
+        // v2: grad scaled by 1/batch, the mean loss left on the device
+        cross_entropy_forward_v2(l.p, t.p, g.p, losses.p, loss_out.p, batch, vocab);
+        const float loss2 = loss_out.get()[0];
+        const std::vector<float> g2 = g.get();
+        float g2_err = 0.0f;
+        for (int i = 0; i < n; ++i) g2_err = std::fmax(g2_err, std::fabs(g2[i] * batch - gref[i]));
+        const float loss2_err = std::fabs(loss_ref - loss2) / (std::fabs(loss_ref) + 1e-8f);
+        check(g2_err < 1e-4f && loss2_err < 1e-2f, "cross-entropy v2 (device loss, grad/batch)",
+              loss2_err);
+    }
+}
+
 int main() {
     test_layernorm();
     test_fusion_pairs();
     test_embedding();
+    test_softmax_ce();
     std::printf("%s (%d failure%s)\n", g_fail ? "FAILED" : "PASSED", g_fail, g_fail == 1 ? "" : "s");
     return g_fail ? 1 : 0;
 }

@@ -6,10 +6,14 @@ and this repository's oracle):
                       (torch.nn.functional.gelu(approximate="tanh") + autograd)
   layernorm_f64.npz   x, gamma, beta, g -> y, dx, dgamma, dbeta for two shapes
                       (torch.nn.functional.layer_norm + autograd, eps=1e-5)
+  softmax_ce_f64.npz  logits, targets -> softmax, per-row cross-entropy, and
+                      its gradient (torch.softmax, torch.nn.functional
+                      .cross_entropy(reduction="none") + autograd)
 
 Inputs are float32 values (stored as float32) so the float paths can consume
 them; torch computes in float64 on those exact values.  Re-run with
-`python tests/golden/make_golden.py` (deterministic; seed fixed below).
+`python tests/golden/make_golden.py [name ...]` (deterministic; seeds fixed
+below; with names, only those fixtures are rewritten).
 """
 import os
 
@@ -49,15 +53,37 @@ def ln_case(rng, rows, cols, tag):
             f"{tag}_dgamma": gt.grad.numpy(), f"{tag}_dbeta": bt.grad.numpy()}
 
 
-def main():
-    rng = np.random.default_rng(20260)
-    np.savez_compressed(os.path.join(HERE, "gelu_tanh_f64.npz"), **gelu_fixture(rng))
-    d = {}
-    d.update(ln_case(rng, 16, 768, "c768"))
-    d.update(ln_case(rng, 9, 33, "c33"))
-    np.savez_compressed(os.path.join(HERE, "layernorm_f64.npz"), **d)
-    print("wrote", os.listdir(HERE))
+def softmax_ce_fixture():
+    rng = np.random.default_rng(20267)
+    rows, cols = 12, 1000
+    logits = (3.0 * rng.standard_normal((rows, cols))).astype(np.float32)
+    logits[1] = 0.5            # a constant row: uniform softmax
+    logits[2, 7] = 60.0        # a dominant logit
+    logits[3] -= 80.0          # large negative offset (needs the max shift)
+    targets = rng.integers(0, cols, rows).astype(np.int32)
+    targets[2] = 7
+    lt = torch.tensor(logits.astype(np.float64), requires_grad=True)
+    sm = torch.softmax(lt, dim=1)
+    loss = torch.nn.functional.cross_entropy(lt, torch.tensor(targets.astype(np.int64)),
+                                             reduction="none")
+    loss.sum().backward()
+    return dict(logits=logits, targets=targets, softmax=sm.detach().numpy(),
+                loss=loss.detach().numpy(), grad=lt.grad.numpy())
+
+
+def main(names):
+    if not names or "gelu_tanh_f64" in names or "layernorm_f64" in names:
+        rng = np.random.default_rng(20260)
+        np.savez_compressed(os.path.join(HERE, "gelu_tanh_f64.npz"), **gelu_fixture(rng))
+        d = {}
+        d.update(ln_case(rng, 16, 768, "c768"))
+        d.update(ln_case(rng, 9, 33, "c33"))
+        np.savez_compressed(os.path.join(HERE, "layernorm_f64.npz"), **d)
+    if not names or "softmax_ce_f64" in names:
+        np.savez_compressed(os.path.join(HERE, "softmax_ce_f64.npz"), **softmax_ce_fixture())
+    print("wrote", sorted(os.listdir(HERE)))
 
 
 if __name__ == "__main__":
-    main()
+    import sys
+    main(sys.argv[1:])

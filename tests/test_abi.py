@@ -55,10 +55,17 @@ def test_host_side_argument_errors():
     assert "NULL" in M.last_error()
     assert lib.mi_gelu_backward_with_bias_backward(None, None, None, None, None, 4, 8,
                                                    None) == M.MI_ERR_INVALID_ARG
+    assert lib.mi_softmax_forward(None, None, 4, 0, None) == M.MI_ERR_INVALID_ARG
+    assert lib.mi_cross_entropy_forward_v2(None, None, None, None, None, 4, 10,
+                                           None) == M.MI_ERR_INVALID_ARG
+    loss = ctypes.c_float(0)
+    assert lib.mi_cross_entropy_forward(None, None, None, -1, 10, ctypes.byref(loss),
+                                        None) == M.MI_ERR_INVALID_ARG
     # empty inputs are a successful no-op
     assert lib.mi_layernorm_forward(None, None, None, None, 0, 768, 1e-5, None) == M.MI_OK
     assert lib.mi_residual_add(None, None, None, 0, None) == M.MI_OK
     assert lib.mi_embedding_forward(None, None, None, 0, 768, 0, None) == M.MI_OK
+    assert lib.mi_softmax_forward(None, None, 0, 10, None) == M.MI_OK
 
 
 def test_workspace_size_queries():
@@ -70,3 +77,4 @@ def test_workspace_size_queries():
     eb = M.lib.mi_embedding_backward_workspace(16384)
     assert eb >= 4 * 16384 * 4
     assert M.lib.mi_layernorm_backward_workspace(0, 768) == 0
+    assert M.lib.mi_cross_entropy_workspace(8192) >= 8192 * 4

@@ -414,3 +414,114 @@ def test_embedding_backwards_are_adjoints_of_the_forwards():
     rhs = float((pos.astype(np.float64)
                  * O.pos_embedding_backward(g, np.zeros((T, D), np.float32), B, T)).sum())
     assert abs(lhs - rhs) <= 1e-4 * (abs(lhs) + 1)
+
+
+# ----------------------------------------------------------------------------
+# Softmax and cross-entropy
+# ----------------------------------------------------------------------------
+
+def _srand42_logits(rows, cols, with_targets):
+    O.lib().orc_srand(42)
+    x = np.empty(rows * cols, np.float32)
+    O.lib().orc_fill_rand_unit(O._p(x), x.size)
+    t = None
+    if with_targets:
+        t = np.empty(rows, np.int32)
+        O.lib().orc_fill_rand_tokens(O._p(t), rows, cols)
+    return x.reshape(rows, cols), t
+
+
+@needs_ref
+def test_softmax_and_cross_entropy_match_reference_cpu_srand42():
+    # NC/tests/test_softmax_ce.cu:77-97 (softmax 256x512) and :125-141
+    # (cross-entropy 128x4096), same srand(42) inputs
+    x, _ = _srand42_logits(256, 512, False)
+    ref = np.empty_like(x)
+    REF.ref_softmax_cpu(O._p(x), O._p(ref), 256, 512)
+    assert np.array_equal(O.softmax_forward(x).view(np.uint32), ref.view(np.uint32))
+
+    logits, t = _srand42_logits(128, 4096, True)
+    gref = np.empty_like(logits)
+    lref = REF.ref_cross_entropy_cpu(O._p(logits), O._p(t), O._p(gref), 128, 4096)
+    loss, grad = O.cross_entropy_cpu(logits, t)
+    assert np.float32(loss).view(np.uint32) == np.float32(lref).view(np.uint32)
+    assert np.array_equal(grad.view(np.uint32), gref.view(np.uint32))
+
+
+@needs_ref
+def test_softmax_matches_reference_cpu_random_shapes():
+    r = rng(31)
+    for rows, cols in ((3, 1), (5, 7), (4, 1025), (2, 50257)):
+        x = (4 * r.standard_normal((rows, cols))).astype(np.float32)
+        ref = np.empty_like(x)
+        REF.ref_softmax_cpu(O._p(x), O._p(ref), rows, cols)
+        assert np.array_equal(O.softmax_forward(x).view(np.uint32), ref.view(np.uint32))
+
+
+def test_softmax_and_cross_entropy_against_torch_golden():
+    d = np.load(os.path.join(GOLDEN, "softmax_ce_f64.npz"))
+    logits, targets = d["logits"], d["targets"]
+    np.testing.assert_allclose(O.softmax_forward_f64(logits), d["softmax"], rtol=1e-12,
+                               atol=1e-300)
+    l64, g64 = O.cross_entropy_f64(logits, targets)
+    np.testing.assert_allclose(l64, d["loss"], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(g64, d["grad"], rtol=1e-12, atol=1e-15)
+    # the float routines at float accuracy
+    np.testing.assert_allclose(O.softmax_forward(logits), d["softmax"], rtol=2e-6, atol=1e-9)
+    losses, grad = O.cross_entropy_rows(logits, targets)
+    # the reference kernel's loss is -log(p[t] + 1e-9), which departs from the
+    # exact cross-entropy by about 1e-9 / p[t]: compare with that formula on
+    # torch's float64 softmax, and bound the departure itself
+    pt = d["softmax"][np.arange(len(targets)), targets]
+    k64 = -np.log(pt + 1e-9)
+    np.testing.assert_allclose(losses, k64, rtol=2e-6, atol=2e-6)
+    assert (np.abs(k64 - d["loss"]) <= 1.01e-9 / pt).all()
+    np.testing.assert_allclose(grad, d["grad"], rtol=2e-6, atol=2e-7)
+    loss_cpu, grad_cpu = O.cross_entropy_cpu(logits, targets)
+    assert abs(loss_cpu - d["loss"].mean()) <= 2e-6 * abs(d["loss"].mean())
+    np.testing.assert_allclose(grad_cpu, d["grad"], rtol=2e-6, atol=2e-7)
+
+
+def test_cross_entropy_rows_invariants():
+    r = rng(33)
+    logits = (2 * r.standard_normal((64, 777))).astype(np.float32)
+    t = r.integers(0, 777, 64).astype(np.int32)
+    losses, g = O.cross_entropy_rows(logits, t)
+    assert (losses > 0).all()
+    # rows of the gradient sum to zero (softmax sums to one)
+    assert np.abs(g.astype(np.float64).sum(1)).max() < 5e-6
+    # the gradient is the softmax minus the one-hot target
+    onehot = np.zeros_like(g)
+    onehot[np.arange(64), t] = 1
+    np.testing.assert_allclose(g + onehot, O.softmax_forward(logits), rtol=1e-6, atol=1e-7)
+    # scale is applied last, to every element
+    _, gs = O.cross_entropy_rows(logits, t, 1 / 64)
+    assert np.array_equal(gs.view(np.uint32), (g * np.float32(1 / 64)).view(np.uint32))
+    # mean in row order
+    acc = np.float32(0)
+    for v in losses:
+        acc = np.float32(acc + v)
+    assert np.float32(O.loss_mean(losses)) == np.float32(acc / np.float32(64))
+    # a target outside the row gives a NaN loss and no one-hot term
+    bad = t.copy()
+    bad[[3, 5]] = [-1, 777]
+    lb, gb = O.cross_entropy_rows(logits, bad)
+    assert np.isnan(lb[[3, 5]]).all() and np.array_equal(lb[:3], losses[:3])
+    g0 = O.cross_entropy_rows(logits[3:4], np.array([0], np.int32))[1][0]
+    np.testing.assert_array_equal(gb[3][1:], g0[1:])
+    assert abs(gb[3][0] - (g0[0] + 1)) < 1e-7
+
+
+def test_planted_mistake_in_cross_entropy_is_caught():
+    d = np.load(os.path.join(GOLDEN, "softmax_ce_f64.npz"))
+    logits, targets = d["logits"].astype(np.float64), d["targets"]
+    p = np.exp(logits - logits.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    onehot = np.zeros_like(p)
+    onehot[np.arange(p.shape[0]), targets] = 1
+    # one-hot added instead of subtracted
+    assert not np.allclose(p + onehot, d["grad"], rtol=1e-4, atol=1e-6)
+    # loss taken at the wrong index (target - 1)
+    wrong_loss = -np.log(p[np.arange(p.shape[0]), targets - 1])
+    assert not np.allclose(wrong_loss, d["loss"], rtol=1e-4)
+    np.testing.assert_allclose(p - onehot, d["grad"], rtol=1e-9, atol=1e-12)
