@@ -23,8 +23,8 @@ Also reported on the same line:
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 --workload picks another BASELINE config (ln, gelu, embedding, block12, xl48,
-wide) or the softmax cross-entropy of the model loss (ce); the default is the
-headline metric.
+wide), the softmax cross-entropy of the model loss (ce) or the optimizer step
+(adam); the default is the headline metric.
 """
 import argparse
 import json
@@ -78,11 +78,13 @@ WORKLOADS = {
     "xl48": "config 4: GPT-2-XL-shaped non-GEMM block x48 layers, [4096,1600] / [4096,6400]",
     "wide": "config 4 wide sweep: LN fwd+bwd [32768,4096]",
     "ce": "softmax cross-entropy of the model loss: logits [8192,50257] (B=8, T=1024, GPT-2 vocab)",
+    "adam": "optimizer step (grad norm^2 + clip + Adam) over GPT-2 small's 124,439,808 parameters",
 }
 
 
 def make_workload(name):
-    from cme213_amd.workloads import BlockSequence, CrossEntropy, Embedding, FwdBwd, Headline
+    from cme213_amd.workloads import (AdamStep, BlockSequence, CrossEntropy, Embedding, FwdBwd,
+                                      Headline)
     if name == "headline":
         return Headline()
     if name == "ln":
@@ -99,6 +101,8 @@ def make_workload(name):
         return FwdBwd(32768, 4096, 0, gelu=False)
     if name == "ce":
         return CrossEntropy()
+    if name == "adam":
+        return AdamStep()
     raise SystemExit(f"unknown workload {name}; choose from {sorted(WORKLOADS)}")
 
 

@@ -103,6 +103,15 @@ _SIGS = {
     "mi_cross_entropy_forward": (c_int, [P, P, P, c_int, c_int, P, P]),
     "mi_cross_entropy_forward_v2": (c_int, [P, P, P, P, P, c_int, c_int, P]),
     "mi_cross_entropy_workspace": (c_size_t, [c_int]),
+    # optimizer
+    "mi_scale_buffer": (c_int, [P, c_float, c_longlong, P]),
+    "mi_buffer_norm_sq_acc": (c_int, [P, c_longlong, P, P]),
+    "mi_compute_clip_scale": (c_int, [P, P, c_float, P]),
+    "mi_adam_clipped": (c_int, [P, P, P, P, P, c_float, c_float, c_float, c_float, c_float,
+                                c_float, c_float, c_longlong, P]),
+    "mi_adam_update": (c_int, [P, P, P, P, c_longlong, c_float, c_float, c_float, c_float, c_int,
+                               c_float, P, P, P]),
+    "mi_norm_sq_workspace": (c_size_t, [c_longlong]),
 }
 
 for _name, (_res, _args) in _SIGS.items():
@@ -299,3 +308,27 @@ def cross_entropy_forward(logits, targets, grad, batch, vocab, stream=None) -> f
 def cross_entropy_forward_v2(logits, targets, grad, losses, loss_out, batch, vocab, stream=None):
     _check(lib.mi_cross_entropy_forward_v2(_f(logits), _i(targets), _f(grad), _f(losses),
                                            _f(loss_out), batch, vocab, _stream(stream)))
+
+
+def scale_buffer(buf, scale, n, stream=None):
+    _check(lib.mi_scale_buffer(_f(buf), scale, n, _stream(stream)))
+
+
+def buffer_norm_sq_acc(buf, n, result, stream=None):
+    _check(lib.mi_buffer_norm_sq_acc(_f(buf), n, _f(result), _stream(stream)))
+
+
+def compute_clip_scale(norm_sq, clip_scale, max_norm, stream=None):
+    _check(lib.mi_compute_clip_scale(_f(norm_sq), _f(clip_scale), max_norm, _stream(stream)))
+
+
+def adam_clipped(param, grad, m, v, clip_scale, lr, beta1, beta2, eps, bc1, bc2, grad_scale, n,
+                 stream=None):
+    _check(lib.mi_adam_clipped(_f(param), _f(grad), _f(m), _f(v), _f(clip_scale), lr, beta1,
+                               beta2, eps, bc1, bc2, grad_scale, n, _stream(stream)))
+
+
+def adam_update(param, grad, m, v, n, lr, beta1, beta2, eps, step, grad_scale, norm_sq,
+                clip_scale, stream=None):
+    _check(lib.mi_adam_update(_f(param), _f(grad), _f(m), _f(v), n, lr, beta1, beta2, eps, step,
+                              grad_scale, _f(norm_sq), _f(clip_scale), _stream(stream)))

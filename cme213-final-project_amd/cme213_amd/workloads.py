@@ -12,7 +12,7 @@ from __future__ import annotations
 
 import torch
 
-from . import (bias_gelu_forward, cross_entropy_forward_v2, embedding_backward,
+from . import (adam_update, bias_gelu_forward, cross_entropy_forward_v2, embedding_backward,
                embedding_pos_forward, gelu_backward_with_bias_backward, layernorm_backward, layernorm_backward_residual,
                layernorm_forward_save, pos_embedding_backward, residual_layernorm_forward_save)
 
@@ -294,6 +294,36 @@ class CrossEntropy:
         s = self.sets[k % len(self.sets)]
         return [("cross_entropy", lambda: cross_entropy_forward_v2(
             s["logits"], s["targets"], s["grad"], s["losses"], s["loss"], self.R, self.V))]
+
+    def step(self, k):
+        for _, fn in self.ops(k):
+            fn()
+
+
+class AdamStep:
+    """The reference's optimizer step, TransformerModel::update_adam
+    (FINAL_CLEAN_CODE/src/model/transformer.cu:619-636), over a flat buffer
+    of GPT-2 small's parameter count: gradient norm², clip scale, clipped
+    Adam.  Algorithmic bytes 4 n (norm² read) + 28 n (Adam: param, grad, m, v
+    read; param, m, v written) = 32 n."""
+
+    def __init__(self, n=124_439_808, seed=20269):
+        self.n = n
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        self.param = _randn((n,), g, 0.02)
+        self.grad = _randn((n,), g, 1e-3)
+        self.m = torch.zeros(n, device="cuda")
+        self.v = torch.zeros(n, device="cuda")
+        self.norm_sq = torch.empty(1, device="cuda")
+        self.clip = torch.empty(1, device="cuda")
+        self.step_bytes = 32 * n
+        self.bytes = {"adam_update": self.step_bytes}
+
+    def ops(self, k):
+        return [("adam_update", lambda: adam_update(self.param, self.grad, self.m, self.v, self.n,
+                                                    3e-4, 0.9, 0.999, 1e-8, k + 1, 1.0,
+                                                    self.norm_sq, self.clip))]
 
     def step(self, k):
         for _, fn in self.ops(k):

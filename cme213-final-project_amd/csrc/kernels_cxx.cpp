@@ -141,3 +141,15 @@ void cross_entropy_forward_v2(const float* logits, const int* targets, float* gr
     MI_CHECK(mi_cross_entropy_forward_v2(logits, targets, grad, d_losses, d_loss_out, batch, vocab,
                                          per_thread_stream()));
 }
+
+void scale_buffer(float* buf, float scale, int n) {
+    MI_CHECK(mi_scale_buffer(buf, scale, n, per_thread_stream()));
+}
+
+void buffer_norm_sq_acc(const float* buf, int n, float* d_result) {
+    MI_CHECK(mi_buffer_norm_sq_acc(buf, n, d_result, per_thread_stream()));
+}
+
+void compute_clip_scale(const float* d_norm_sq, float* d_clip_scale, float max_norm) {
+    MI_CHECK(mi_compute_clip_scale(d_norm_sq, d_clip_scale, max_norm, per_thread_stream()));
+}

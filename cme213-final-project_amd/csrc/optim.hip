@@ -1,0 +1,268 @@
+// Optimizer step over the flat parameter buffer for gfx950: gradient norm²,
+// clip scale, clipped Adam, and buffer scaling.
+//
+// Reference behaviour:
+//  * scale_buffer (FINAL_CLEAN_CODE/src/kernels/activations.cu:349-358):
+//    buf[i] *= scale;
+//  * buffer_norm_sq_acc (:360-381): *d_result += sum buf[i]^2, one
+//    atomicAdd per 512-element block (the caller zeroes *d_result first);
+//  * compute_clip_scale (:383-392): c = sqrt(n2) > max ? max / sqrt(n2) : 1;
+//  * adam_clipped_kernel / update_adam (src/model/transformer.cu:598-636):
+//    g = grad * grad_scale * c; m = b1 m + (1 - b1) g;
+//    v = b2 v + (1 - b2) g g; p -= lr (m / bc1) / (sqrt(v / bc2) + eps),
+//    after memset + norm + clip kernels.
+//
+// Here the norm² is a deterministic two-pass sum (per-workgroup partials in
+// the library workspace, then one workgroup adding them in a fixed order,
+// which can also derive the clip scale), and Adam is one grid-stride pass of
+// 16-byte vectors.  The Adam arithmetic is evaluated exactly as written
+// (no FMA contraction), so it is bit-identical to the CPU statement of the
+// reference kernel given the same clip scale.
+#include "mi_common.hpp"
+
+namespace mi {
+
+namespace {
+
+constexpr int kOptThreads = 256;
+constexpr int kNormBlocks = 1024;  // partial sums of the norm² pass
+constexpr int kFinThreads = 1024;
+
+// ----- sum of squares --------------------------------------------------------
+
+template <int W>
+__global__ __launch_bounds__(kOptThreads) void sumsq_partial_kernel(const float* __restrict__ buf,
+                                                                    long long nvec,
+                                                                    float* __restrict__ part) {
+    __shared__ float red[kOptThreads / kWave];
+    // One running sum per vector component keeps each sequential chain short.
+    float acc[W];
+#pragma unroll
+    for (int e = 0; e < W; ++e) acc[e] = 0.0f;
+    const long long stride = static_cast<long long>(gridDim.x) * kOptThreads;
+    for (long long i = static_cast<long long>(blockIdx.x) * kOptThreads + threadIdx.x; i < nvec;
+         i += stride) {
+        const fvec<W> x = sload<W>(buf, static_cast<size_t>(i));
+#pragma unroll
+        for (int e = 0; e < W; ++e) acc[e] += x.v[e] * x.v[e];
+    }
+    float s = acc[0];
+#pragma unroll
+    for (int e = 1; e < W; ++e) s += acc[e];
+    s = wave_sum(s);
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float t = red[0];
+#pragma unroll
+        for (int w = 1; w < kOptThreads / kWave; ++w) t += red[w];
+        part[blockIdx.x] = t;
+    }
+}
+
+// Adds the P partials in a fixed order and stores the total in *result,
+// added to its old value when `accumulate` (the reference's `+=` contract);
+// if clip != nullptr, also writes the clip scale for max_norm.
+__global__ __launch_bounds__(kFinThreads) void sumsq_finalize_kernel(
+    const float* __restrict__ part, int P, float* __restrict__ result, bool accumulate,
+    float* __restrict__ clip, float max_norm) {
+    __shared__ float red[kFinThreads / kWave];
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < P; i += kFinThreads) s += part[i];
+    s = wave_sum(s);
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float t = red[0];
+#pragma unroll
+        for (int w = 1; w < kFinThreads / kWave; ++w) t += red[w];
+        const float total = accumulate ? *result + t : t;
+        *result = total;
+        if (clip) {
+            const float norm = sqrtf(total);
+            *clip = (norm > max_norm) ? (max_norm / norm) : 1.0f;
+        }
+    }
+}
+
+__global__ void clip_scale_kernel(const float* __restrict__ norm_sq, float* __restrict__ clip,
+                                  float max_norm) {
+    const float norm = sqrtf(*norm_sq);
+    *clip = (norm > max_norm) ? (max_norm / norm) : 1.0f;
+}
+
+// ----- Adam ------------------------------------------------------------------
+
+struct AdamArgs {
+    float lr, beta1, beta2, eps, bc1, bc2, grad_scale;
+};
+
+template <int W>
+__global__ __launch_bounds__(kOptThreads) void adam_kernel(float* __restrict__ param,
+                                                           const float* __restrict__ grad,
+                                                           float* __restrict__ m,
+                                                           float* __restrict__ v,
+                                                           const float* __restrict__ clip,
+                                                           AdamArgs a, long long nvec) {
+#pragma clang fp contract(off)
+    const float c = *clip;
+    const long long stride = static_cast<long long>(gridDim.x) * kOptThreads;
+    for (long long i = static_cast<long long>(blockIdx.x) * kOptThreads + threadIdx.x; i < nvec;
+         i += stride) {
+        const size_t k = static_cast<size_t>(i);
+        const fvec<W> gv = sload<W>(grad, k), mv = sload<W>(m, k), vv = sload<W>(v, k);
+        fvec<W> pv = sload<W>(param, k), mo, vo;
+#pragma unroll
+        for (int e = 0; e < W; ++e) {
+            const float g = gv.v[e] * a.grad_scale * c;
+            const float mi = a.beta1 * mv.v[e] + (1.0f - a.beta1) * g;
+            const float vi = a.beta2 * vv.v[e] + (1.0f - a.beta2) * g * g;
+            mo.v[e] = mi;
+            vo.v[e] = vi;
+            const float m_hat = mi / a.bc1;
+            const float v_hat = vi / a.bc2;
+            pv.v[e] = pv.v[e] - a.lr * m_hat / (sqrtf(v_hat) + a.eps);
+        }
+        sstore<W>(m, k, mo);
+        sstore<W>(v, k, vo);
+        sstore<W>(param, k, pv);
+    }
+}
+
+template <int W>
+__global__ __launch_bounds__(kOptThreads) void scale_kernel(float* __restrict__ buf, float scale,
+                                                            long long nvec) {
+    const long long stride = static_cast<long long>(gridDim.x) * kOptThreads;
+    for (long long i = static_cast<long long>(blockIdx.x) * kOptThreads + threadIdx.x; i < nvec;
+         i += stride) {
+        fvec<W> x = sload<W>(buf, static_cast<size_t>(i));
+#pragma unroll
+        for (int e = 0; e < W; ++e) x.v[e] = x.v[e] * scale;
+        sstore<W>(buf, static_cast<size_t>(i), x);
+    }
+}
+
+unsigned flat_grid(long long nvec, int cap) {
+    long long g = (nvec + kOptThreads - 1) / kOptThreads;
+    if (g > cap) g = cap;
+    return static_cast<unsigned>(g < 1 ? 1 : g);
+}
+
+// Partial rows of the norm² pass: depends only on n, so the summation
+// order is fixed for a given n.
+int norm_blocks(long long nvec) { return static_cast<int>(flat_grid(nvec, kNormBlocks)); }
+
+int sumsq_impl(const char* name, const float* buf, long long n, float* result, bool accumulate,
+               float* clip, float max_norm, hipStream_t st) {
+    if (n < 0) return set_error(MI_ERR_INVALID_ARG, "%s: n=%lld", name, n);
+    if (!result || (n > 0 && !buf)) return set_error(MI_ERR_INVALID_ARG, "%s: NULL pointer", name);
+    const bool vec4 = n % 4 == 0 && aligned16(buf);
+    const long long nvec = vec4 ? n / 4 : n;
+    const int P = norm_blocks(nvec);
+    int err = MI_OK;
+    char* ws = static_cast<char*>(
+        workspace_get(colsum_part_offset() + static_cast<size_t>(P) * sizeof(float), st, &err));
+    if (!ws) return err;
+    float* part = reinterpret_cast<float*>(ws + colsum_part_offset());
+    if (vec4)
+        hipLaunchKernelGGL(sumsq_partial_kernel<4>, dim3(P), dim3(kOptThreads), 0, st, buf, nvec,
+                           part);
+    else
+        hipLaunchKernelGGL(sumsq_partial_kernel<1>, dim3(P), dim3(kOptThreads), 0, st, buf, nvec,
+                           part);
+    int rc = check_launch(name);
+    if (rc != MI_OK) return rc;
+    hipLaunchKernelGGL(sumsq_finalize_kernel, dim3(1), dim3(kFinThreads), 0, st, part, P, result,
+                       accumulate, clip, max_norm);
+    return check_launch(name);
+}
+
+int adam_impl(const char* name, float* param, const float* grad, float* m, float* v,
+              const float* clip, const AdamArgs& a, long long n, hipStream_t st) {
+    if (n < 0) return set_error(MI_ERR_INVALID_ARG, "%s: n=%lld", name, n);
+    if (n == 0) return MI_OK;
+    if (!param || !grad || !m || !v || !clip)
+        return set_error(MI_ERR_INVALID_ARG, "%s: NULL pointer", name);
+    const bool vec4 = n % 4 == 0 && aligned16(param) && aligned16(grad) && aligned16(m) &&
+                      aligned16(v);
+    const long long nvec = vec4 ? n / 4 : n;
+    const dim3 grid(flat_grid(nvec, 16384));
+    if (vec4)
+        hipLaunchKernelGGL(adam_kernel<4>, grid, dim3(kOptThreads), 0, st, param, grad, m, v, clip,
+                           a, nvec);
+    else
+        hipLaunchKernelGGL(adam_kernel<1>, grid, dim3(kOptThreads), 0, st, param, grad, m, v, clip,
+                           a, nvec);
+    return check_launch(name);
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" {
+
+int mi_scale_buffer(float* buf, float scale, long long n, void* stream) {
+    const char* name = "mi_scale_buffer";
+    if (n < 0) return set_error(MI_ERR_INVALID_ARG, "%s: n=%lld", name, n);
+    if (n == 0) return MI_OK;
+    if (!buf) return set_error(MI_ERR_INVALID_ARG, "%s: NULL pointer", name);
+    hipStream_t st = to_stream(stream);
+    if (n % 4 == 0 && aligned16(buf))
+        hipLaunchKernelGGL(scale_kernel<4>, dim3(flat_grid(n / 4, 16384)), dim3(kOptThreads), 0,
+                           st, buf, scale, n / 4);
+    else
+        hipLaunchKernelGGL(scale_kernel<1>, dim3(flat_grid(n, 16384)), dim3(kOptThreads), 0, st,
+                           buf, scale, n);
+    return check_launch(name);
+}
+
+int mi_buffer_norm_sq_acc(const float* buf, long long n, float* d_result, void* stream) {
+    return sumsq_impl("mi_buffer_norm_sq_acc", buf, n, d_result, true, nullptr, 0.0f,
+                      to_stream(stream));
+}
+
+int mi_compute_clip_scale(const float* d_norm_sq, float* d_clip_scale, float max_norm,
+                          void* stream) {
+    const char* name = "mi_compute_clip_scale";
+    if (!d_norm_sq || !d_clip_scale) return set_error(MI_ERR_INVALID_ARG, "%s: NULL", name);
+    hipLaunchKernelGGL(clip_scale_kernel, dim3(1), dim3(1), 0, to_stream(stream), d_norm_sq,
+                       d_clip_scale, max_norm);
+    return check_launch(name);
+}
+
+int mi_adam_clipped(float* param, const float* grad, float* m, float* v,
+                    const float* d_clip_scale, float lr, float beta1, float beta2, float eps,
+                    float bc1, float bc2, float grad_scale, long long n, void* stream) {
+    return adam_impl("mi_adam_clipped", param, grad, m, v, d_clip_scale,
+                     AdamArgs{lr, beta1, beta2, eps, bc1, bc2, grad_scale}, n, to_stream(stream));
+}
+
+int mi_adam_update(float* param, const float* grad, float* m, float* v, long long n, float lr,
+                   float beta1, float beta2, float eps, int step, float grad_scale,
+                   float* d_norm_sq, float* d_clip_scale, void* stream) {
+    const char* name = "mi_adam_update";
+    if (step < 1) return set_error(MI_ERR_INVALID_ARG, "%s: step=%d (must be >= 1)", name, step);
+    if (!d_norm_sq || !d_clip_scale)
+        return set_error(MI_ERR_INVALID_ARG, "%s: NULL norm / clip pointer", name);
+    hipStream_t st = to_stream(stream);
+    // transformer.cu:619-636: bias corrections on the host, the norm² from
+    // zero, clip max norm 1 / grad_scale (1 when grad_scale <= 0).
+    const float bc1 = 1.0f - powf(beta1, static_cast<float>(step));
+    const float bc2 = 1.0f - powf(beta2, static_cast<float>(step));
+    const float max_norm = (grad_scale > 0.0f) ? (1.0f / grad_scale) : 1.0f;
+    // The reference zeroes *d_norm_sq with a memset and accumulates into it;
+    // here the finalize overwrites it, so no memset node is needed.
+    int rc = sumsq_impl(name, grad, n, d_norm_sq, false, d_clip_scale, max_norm, st);
+    if (rc != MI_OK) return rc;
+    return adam_impl(name, param, grad, m, v, d_clip_scale,
+                     AdamArgs{lr, beta1, beta2, eps, bc1, bc2, grad_scale}, n, st);
+}
+
+size_t mi_norm_sq_workspace(long long n) {
+    if (n <= 0) return 0;
+    return colsum_part_offset() + static_cast<size_t>(norm_blocks(n)) * sizeof(float);
+}
+
+}  // extern "C"

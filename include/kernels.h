@@ -23,7 +23,9 @@
 //    reduces the mean loss in a fixed order in one kernel (no memset, no
 //    atomics);
 //  * a cross-entropy target outside [0, vocab) gives a NaN loss instead of
-//    an out-of-bounds access.
+//    an out-of-bounds access;
+//  * buffer_norm_sq_acc sums in a fixed order (two passes through the
+//    library workspace) instead of with float atomics.
 // The same kernels are reachable through the C ABI in mi_kernels.h.
 #pragma once
 
@@ -85,6 +87,11 @@ void bias_gelu_forward(const float* in, const float* bias, float* out,
 void gelu_backward_with_bias_backward(const float* in, const float* bias,
                                       const float* grad_out, float* grad_in,
                                       float* dbias, int rows, int cols);
+
+// --- optimizer helpers (reference kernels.h:113-120) ------------------------
+void scale_buffer(float* buf, float scale, int n);
+void buffer_norm_sq_acc(const float* buf, int n, float* d_result);
+void compute_clip_scale(const float* d_norm_sq, float* d_clip_scale, float max_norm);
 
 // --- softmax / cross-entropy (reference kernels.h:122-129) -----------------
 void softmax_forward(const float* x, float* out, int rows, int cols);

@@ -213,6 +213,43 @@ int mi_cross_entropy_forward_v2(const float* logits, const int* targets, float* 
 /* Workspace bytes mi_cross_entropy_forward needs for `batch` rows. */
 size_t mi_cross_entropy_workspace(int batch);
 
+/* ----- optimizer step over the flat parameter buffer ---------------------- */
+
+/* buf[i] *= scale.  Replaces scale_buffer (kernels.h:113,
+ * FINAL_CLEAN_CODE/src/kernels/activations.cu:349-358). */
+int mi_scale_buffer(float* buf, float scale, long long n, void* stream);
+
+/* *d_result += sum of buf[i]^2, with a deterministic two-pass sum (per-block
+ * partials in the library workspace, then a fixed-order total) instead of
+ * the reference's per-block float atomicAdd.  Replaces buffer_norm_sq_acc
+ * (kernels.h:118, activations.cu:360-381). */
+int mi_buffer_norm_sq_acc(const float* buf, long long n, float* d_result, void* stream);
+
+/* *d_clip_scale = sqrt(*d_norm_sq) > max_norm ? max_norm / sqrt(*d_norm_sq)
+ * : 1.  Replaces compute_clip_scale (kernels.h:120, activations.cu:383-392). */
+int mi_compute_clip_scale(const float* d_norm_sq, float* d_clip_scale, float max_norm,
+                          void* stream);
+
+/* One clipped Adam step, the arithmetic of adam_clipped_kernel
+ * (FINAL_CLEAN_CODE/src/model/transformer.cu:598-617) evaluated as written:
+ * g = grad * grad_scale * (*d_clip_scale); m = beta1 m + (1 - beta1) g;
+ * v = beta2 v + (1 - beta2) g g; param -= lr (m / bc1) / (sqrt(v / bc2) + eps). */
+int mi_adam_clipped(float* param, const float* grad, float* m, float* v,
+                    const float* d_clip_scale, float lr, float beta1, float beta2, float eps,
+                    float bc1, float bc2, float grad_scale, long long n, void* stream);
+
+/* TransformerModel::update_adam (transformer.cu:619-636) in one call: bias
+ * corrections 1 - beta^step on the host, the gradient norm² into *d_norm_sq
+ * (overwritten, no memset), the clip scale for max norm 1 / grad_scale (1
+ * when grad_scale <= 0) into *d_clip_scale, then the Adam step.  Three
+ * kernels, graph-capturable; step >= 1. */
+int mi_adam_update(float* param, const float* grad, float* m, float* v, long long n, float lr,
+                   float beta1, float beta2, float eps, int step, float grad_scale,
+                   float* d_norm_sq, float* d_clip_scale, void* stream);
+
+/* Workspace bytes mi_buffer_norm_sq_acc / mi_adam_update need for n floats. */
+size_t mi_norm_sq_workspace(long long n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -563,3 +563,50 @@ void orc_softmax_forward_f64(const float* x, double* out, int rows, int cols) {
         for (int c = 0; c < cols; ++c) out[(long)r * cols + c] = exp((double)row[c] - m) / s;
     }
 }
+
+/* ----- optimizer step ------------------------------------------------------ */
+
+/* buf[i] *= scale, FC/src/kernels/activations.cu:349-352. */
+void orc_scale_buffer(float* buf, float scale, long n) {
+    for (long i = 0; i < n; ++i) buf[i] *= scale;
+}
+
+/* Sum of squares in double.  The reference accumulates float block sums
+ * with atomicAdd (activations.cu:360-375), which has no fixed order; the
+ * tests hold float results to a relative bound against this value. */
+double orc_sumsq_f64(const float* buf, long n) {
+    double s = 0.0;
+    for (long i = 0; i < n; ++i) s += (double)buf[i] * (double)buf[i];
+    return s;
+}
+
+/* Clip scale, FC/src/kernels/activations.cu:383-387. */
+float orc_clip_scale(float norm_sq, float max_norm) {
+    float norm = sqrtf(norm_sq);
+    return (norm > max_norm) ? (max_norm / norm) : 1.0f;
+}
+
+/* One clipped Adam step, FC/src/model/transformer.cu:598-617 statement for
+ * statement (clip scale passed by value instead of through a device
+ * pointer). */
+void orc_adam_clipped(float* param, const float* grad, float* m, float* v, float clip,
+                      float lr, float beta1, float beta2, float eps, float bc1, float bc2,
+                      float grad_scale, long n) {
+    for (long i = 0; i < n; ++i) {
+        float g = grad[i] * grad_scale * clip;
+        float mi = beta1 * m[i] + (1.0f - beta1) * g;
+        float vi = beta2 * v[i] + (1.0f - beta2) * g * g;
+        m[i] = mi;
+        v[i] = vi;
+        float m_hat = mi / bc1;
+        float v_hat = vi / bc2;
+        param[i] -= lr * m_hat / (sqrtf(v_hat) + eps);
+    }
+}
+
+/* Host bias corrections of TransformerModel::update_adam
+ * (FC/src/model/transformer.cu:621-622): 1 - powf(beta, step). */
+void orc_adam_bias_corrections(float beta1, float beta2, int step, float* bc1, float* bc2) {
+    *bc1 = 1.0f - powf(beta1, (float)step);
+    *bc2 = 1.0f - powf(beta2, (float)step);
+}

@@ -65,9 +65,16 @@ def lib():
             "orc_cross_entropy_rows": [P, P, P, P, c_int, c_int, c_float],
             "orc_loss_mean": [P, c_int],
             "orc_cross_entropy_f64": [P, P, P, P, c_int, c_int],
+            "orc_scale_buffer": [P, c_float, c_long],
+            "orc_sumsq_f64": [P, c_long],
+            "orc_clip_scale": [c_float, c_float],
+            "orc_adam_clipped": [P, P, P, P, c_float, c_float, c_float, c_float, c_float,
+                                 c_float, c_float, c_float, c_long],
+            "orc_adam_bias_corrections": [c_float, c_float, c_int, P, P],
         }
         restypes = {"orc_get_threads": c_int, "orc_cross_entropy_cpu": c_float,
-                    "orc_loss_mean": c_float}
+                    "orc_loss_mean": c_float, "orc_sumsq_f64": c_double,
+                    "orc_clip_scale": c_float}
         for name, args in sigs.items():
             fn = getattr(L, name)
             fn.argtypes = args
@@ -378,3 +385,35 @@ def cross_entropy_f64(logits, targets):
     lib().orc_cross_entropy_f64(_p(logits), _p(targets), _p(grad), _p(losses), logits.shape[0],
                                 logits.shape[1])
     return losses, grad
+
+
+# ----- optimizer step ----------------------------------------------------------
+
+def scale_buffer(buf, scale):
+    out = f32(buf).copy()
+    lib().orc_scale_buffer(_p(out), scale, out.size)
+    return out
+
+
+def sumsq_f64(buf):
+    buf = f32(buf)
+    return float(lib().orc_sumsq_f64(_p(buf), buf.size))
+
+
+def clip_scale(norm_sq, max_norm):
+    return float(lib().orc_clip_scale(norm_sq, max_norm))
+
+
+def adam_clipped(param, grad, m, v, clip, lr, beta1, beta2, eps, bc1, bc2, grad_scale):
+    """Returns updated (param, m, v) copies."""
+    p_, m_, v_ = f32(param).copy(), f32(m).copy(), f32(v).copy()
+    grad = f32(grad)
+    lib().orc_adam_clipped(_p(p_), _p(grad), _p(m_), _p(v_), clip, lr, beta1, beta2, eps, bc1,
+                           bc2, grad_scale, p_.size)
+    return p_, m_, v_
+
+
+def adam_bias_corrections(beta1, beta2, step):
+    b1, b2 = ctypes.c_float(0), ctypes.c_float(0)
+    lib().orc_adam_bias_corrections(beta1, beta2, step, ctypes.byref(b1), ctypes.byref(b2))
+    return b1.value, b2.value

@@ -61,6 +61,9 @@ def test_host_side_argument_errors():
     loss = ctypes.c_float(0)
     assert lib.mi_cross_entropy_forward(None, None, None, -1, 10, ctypes.byref(loss),
                                         None) == M.MI_ERR_INVALID_ARG
+    assert lib.mi_adam_update(None, None, None, None, 10, 1e-3, 0.9, 0.999, 1e-8, 0, 1.0, None,
+                              None, None) == M.MI_ERR_INVALID_ARG
+    assert lib.mi_scale_buffer(None, 2.0, -1, None) == M.MI_ERR_INVALID_ARG
     # empty inputs are a successful no-op
     assert lib.mi_layernorm_forward(None, None, None, None, 0, 768, 1e-5, None) == M.MI_OK
     assert lib.mi_residual_add(None, None, None, 0, None) == M.MI_OK

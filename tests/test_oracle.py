@@ -525,3 +525,77 @@ def test_planted_mistake_in_cross_entropy_is_caught():
     wrong_loss = -np.log(p[np.arange(p.shape[0]), targets - 1])
     assert not np.allclose(wrong_loss, d["loss"], rtol=1e-4)
     np.testing.assert_allclose(p - onehot, d["grad"], rtol=1e-9, atol=1e-12)
+
+
+# ----------------------------------------------------------------------------
+# Optimizer step
+# ----------------------------------------------------------------------------
+
+def _torch_adam_f64(p, g_eff, m, v, lr, b1, b2, eps, steps_done):
+    """torch.optim.Adam (float64, CPU): an independent implementation.  The
+    moment buffers and step count are seeded from (m, v, steps_done)."""
+    import torch
+    pt = torch.tensor(p.astype(np.float64), requires_grad=True)
+    opt = torch.optim.Adam([pt], lr=lr, betas=(b1, b2), eps=eps)
+    pt.grad = torch.tensor(g_eff)
+    if steps_done:
+        st = opt.state[pt]
+        st["step"] = torch.tensor(float(steps_done), dtype=torch.float64)
+        st["exp_avg"] = torch.tensor(m.astype(np.float64))
+        st["exp_avg_sq"] = torch.tensor(v.astype(np.float64))
+    opt.step()
+    st = opt.state[pt]
+    return pt.detach().numpy(), st["exp_avg"].numpy(), st["exp_avg_sq"].numpy()
+
+
+@pytest.mark.parametrize("step", [1, 7])
+def test_adam_against_torch_optim_f64(step):
+    r = rng(41 + step)
+    n = 5000
+    p = r.standard_normal(n).astype(np.float32)
+    grad = (3 * r.standard_normal(n)).astype(np.float32)
+    m = (0.1 * r.standard_normal(n)).astype(np.float32) if step > 1 else np.zeros(n, np.float32)
+    v = (0.01 * r.random(n)).astype(np.float32) if step > 1 else np.zeros(n, np.float32)
+    lr, b1, b2, eps, grad_scale = 3e-4, 0.9, 0.999, 1e-8, 0.5
+    norm_sq = O.sumsq_f64(grad)
+    max_norm = 1.0 / grad_scale
+    clip = O.clip_scale(np.float32(norm_sq), max_norm)
+    assert abs(clip - min(1.0, max_norm / np.sqrt(norm_sq))) < 1e-6
+    bc1, bc2 = O.adam_bias_corrections(b1, b2, step)
+    assert abs(bc1 - (1 - b1 ** step)) < 1e-6 and abs(bc2 - (1 - b2 ** step)) < 1e-6
+    po, mo, vo = O.adam_clipped(p, grad, m, v, clip, lr, b1, b2, eps, bc1, bc2, grad_scale)
+    g_eff = grad.astype(np.float64) * grad_scale * clip
+    # torch gets the hyper-parameters as the float kernel sees them
+    f = lambda a: float(np.float32(a))
+    pt, mt, vt = _torch_adam_f64(p, g_eff, m, v, f(lr), f(b1), f(b2), f(eps), step - 1)
+    np.testing.assert_allclose(mo, mt, rtol=1e-6, atol=1e-9)
+    np.testing.assert_allclose(vo, vt, rtol=1e-5, atol=1e-12)
+    # the updated parameter: one float rounding of p - update (|p| ulp) plus
+    # a relative error of the update (at most lr / (1 - b1^t) in size)
+    bound = 1.2e-7 * np.abs(p) + 1e-4 * np.abs(pt - p) + 1e-12
+    assert (np.abs(po - pt) <= bound).all()
+
+
+def test_planted_mistake_in_adam_is_caught():
+    r = rng(47)
+    n = 2000
+    p = r.standard_normal(n).astype(np.float32)
+    grad = r.standard_normal(n).astype(np.float32)
+    z = np.zeros(n, np.float32)
+    lr, b1, b2, eps = 1e-3, 0.9, 0.999, 1e-8
+    f = lambda a: float(np.float32(a))
+    pt, _, _ = _torch_adam_f64(p, grad.astype(np.float64), z, z, f(lr), f(b1), f(b2), f(eps), 0)
+    # bias corrections left out (bc = 1)
+    wrong, _, _ = O.adam_clipped(p, grad, z, z, 1.0, lr, b1, b2, eps, 1.0, 1.0, 1.0)
+    bound = 1.2e-7 * np.abs(p) + 1e-4 * np.abs(pt - p) + 1e-12
+    assert not (np.abs(wrong - pt) <= bound).all()
+    bc1, bc2 = O.adam_bias_corrections(b1, b2, 1)
+    right, _, _ = O.adam_clipped(p, grad, z, z, 1.0, lr, b1, b2, eps, bc1, bc2, 1.0)
+    assert (np.abs(right - pt) <= bound).all()
+
+
+def test_scale_and_sumsq():
+    r = rng(49)
+    x = r.standard_normal(1001).astype(np.float32)
+    assert np.array_equal(O.scale_buffer(x, 0.25).view(np.uint32), (x * np.float32(0.25)).view(np.uint32))
+    assert abs(O.sumsq_f64(x) - float((x.astype(np.float64) ** 2).sum())) < 1e-9
