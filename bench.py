@@ -23,8 +23,9 @@ Also reported on the same line:
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 --workload picks another BASELINE config (ln, gelu, embedding, block12, xl48,
-wide), the softmax cross-entropy of the model loss (ce) or the optimizer step
-(adam); the default is the headline metric.
+wide), the softmax cross-entropy of the model loss (ce), the optimizer step
+(adam) or the fp16 activation-storage path (relu16); the default is the
+headline metric.
 """
 import argparse
 import json
@@ -79,12 +80,13 @@ WORKLOADS = {
     "wide": "config 4 wide sweep: LN fwd+bwd [32768,4096]",
     "ce": "softmax cross-entropy of the model loss: logits [8192,50257] (B=8, T=1024, GPT-2 vocab)",
     "adam": "optimizer step (grad norm^2 + clip + Adam) over GPT-2 small's 124,439,808 parameters",
+    "relu16": "fp16 activation storage: bias+ReLU to half fwd + half-mask ReLU bwd+dbias [8192,3072]",
 }
 
 
 def make_workload(name):
     from cme213_amd.workloads import (AdamStep, BlockSequence, CrossEntropy, Embedding, FwdBwd,
-                                      Headline)
+                                      Headline, Relu16)
     if name == "headline":
         return Headline()
     if name == "ln":
@@ -103,6 +105,8 @@ def make_workload(name):
         return CrossEntropy()
     if name == "adam":
         return AdamStep()
+    if name == "relu16":
+        return Relu16()
     raise SystemExit(f"unknown workload {name}; choose from {sorted(WORKLOADS)}")
 
 

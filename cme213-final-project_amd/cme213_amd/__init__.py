@@ -112,6 +112,15 @@ _SIGS = {
     "mi_adam_update": (c_int, [P, P, P, P, c_longlong, c_float, c_float, c_float, c_float, c_int,
                                c_float, P, P, P]),
     "mi_norm_sq_workspace": (c_size_t, [c_longlong]),
+    # 16-bit storage
+    "mi_float_to_half": (c_int, [P, P, c_longlong, P]),
+    "mi_half_to_float": (c_int, [P, P, c_longlong, P]),
+    "mi_float_to_bf16": (c_int, [P, P, c_longlong, P]),
+    "mi_bf16_to_float": (c_int, [P, P, c_longlong, P]),
+    "mi_bias_relu_forward_to_half": (c_int, [P, P, P, c_int, c_int, P]),
+    "mi_bias_gelu_forward_to_half": (c_int, [P, P, P, c_int, c_int, P]),
+    "mi_bias_gelu_forward_to_bf16": (c_int, [P, P, P, c_int, c_int, P]),
+    "mi_relu_backward_with_bias_backward_half_mask": (c_int, [P, P, P, P, c_int, c_int, P]),
 }
 
 for _name, (_res, _args) in _SIGS.items():
@@ -332,3 +341,49 @@ def adam_update(param, grad, m, v, n, lr, beta1, beta2, eps, step, grad_scale, n
                 clip_scale, stream=None):
     _check(lib.mi_adam_update(_f(param), _f(grad), _f(m), _f(v), n, lr, beta1, beta2, eps, step,
                               grad_scale, _f(norm_sq), _f(clip_scale), _stream(stream)))
+
+
+def _h(x):
+    """16-bit buffer: a torch float16 / bfloat16 tensor (or int address)."""
+    import torch
+    if isinstance(x, torch.Tensor) and x.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"expected a float16 or bfloat16 tensor, got {x.dtype}")
+    return _ptr(x)
+
+
+def float_to_half(inp, out16, n, stream=None):
+    _check(lib.mi_float_to_half(_f(inp), _h(out16), n, _stream(stream)))
+
+
+def half_to_float(in16, out, n, stream=None):
+    _check(lib.mi_half_to_float(_h(in16), _f(out), n, _stream(stream)))
+
+
+def float_to_bf16(inp, out16, n, stream=None):
+    _check(lib.mi_float_to_bf16(_f(inp), _h(out16), n, _stream(stream)))
+
+
+def bf16_to_float(in16, out, n, stream=None):
+    _check(lib.mi_bf16_to_float(_h(in16), _f(out), n, _stream(stream)))
+
+
+def bias_relu_forward_to_half(inp, bias, out16, rows, cols, stream=None):
+    _check(lib.mi_bias_relu_forward_to_half(_f(inp), _f(bias), _h(out16), rows, cols,
+                                            _stream(stream)))
+
+
+def bias_gelu_forward_to_half(inp, bias, out16, rows, cols, stream=None):
+    _check(lib.mi_bias_gelu_forward_to_half(_f(inp), _f(bias), _h(out16), rows, cols,
+                                            _stream(stream)))
+
+
+def bias_gelu_forward_to_bf16(inp, bias, out16, rows, cols, stream=None):
+    _check(lib.mi_bias_gelu_forward_to_bf16(_f(inp), _f(bias), _h(out16), rows, cols,
+                                            _stream(stream)))
+
+
+def relu_backward_with_bias_backward_half_mask(mask16, grad_out, grad_in, dbias, rows, cols,
+                                               stream=None):
+    _check(lib.mi_relu_backward_with_bias_backward_half_mask(_h(mask16), _f(grad_out),
+                                                             _f(grad_in), _f(dbias), rows, cols,
+                                                             _stream(stream)))

@@ -12,9 +12,11 @@ from __future__ import annotations
 
 import torch
 
-from . import (adam_update, bias_gelu_forward, cross_entropy_forward_v2, embedding_backward,
-               embedding_pos_forward, gelu_backward_with_bias_backward, layernorm_backward, layernorm_backward_residual,
-               layernorm_forward_save, pos_embedding_backward, residual_layernorm_forward_save)
+from . import (adam_update, bias_gelu_forward, bias_relu_forward_to_half,
+               cross_entropy_forward_v2, embedding_backward, embedding_pos_forward,
+               gelu_backward_with_bias_backward, layernorm_backward, layernorm_backward_residual,
+               layernorm_forward_save, pos_embedding_backward,
+               relu_backward_with_bias_backward_half_mask, residual_layernorm_forward_save)
 
 F32 = 4
 
@@ -324,6 +326,38 @@ class AdamStep:
         return [("adam_update", lambda: adam_update(self.param, self.grad, self.m, self.v, self.n,
                                                     3e-4, 0.9, 0.999, 1e-8, k + 1, 1.0,
                                                     self.norm_sq, self.clip))]
+
+    def step(self, k):
+        for _, fn in self.ops(k):
+            fn()
+
+
+class Relu16:
+    """The reference's fp16 activation-storage path at config 1's shape
+    (FINAL_CLEAN_CODE/src/kernels/activations.cu:199-217,285-323):
+    bias_relu_forward_to_half (fp32 in, fp16 out) and
+    relu_backward_with_bias_backward_half_mask (fp16 mask, fp32 grads) on
+    [8192, 3072].  Bytes: fwd 4N + 2N + 4F, bwd 2N + 4N + 4N + 8F."""
+
+    def __init__(self, R=8192, F=3072, sets=4, seed=20270):
+        self.R, self.F = R, F
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        self.bias = _randn((F,), g, 0.02)
+        self.dbias = torch.zeros(F, device="cuda")
+        self.sets = [{"h": _randn((R, F), g, 1.5), "dh": _randn((R, F), g),
+                      "o16": torch.empty(R, F, dtype=torch.float16, device="cuda"),
+                      "gin": torch.empty(R, F, device="cuda")} for _ in range(sets)]
+        N = R * F
+        self.bytes = {"relu16_fwd": 6 * N + F32 * F, "relu16_bwd": 10 * N + 8 * F}
+        self.step_bytes = sum(self.bytes.values())
+
+    def ops(self, k):
+        s, p = self.sets[k % len(self.sets)], self.sets[(k - 1) % len(self.sets)]
+        R, F = self.R, self.F
+        return [("relu16_fwd", lambda: bias_relu_forward_to_half(s["h"], self.bias, s["o16"], R, F)),
+                ("relu16_bwd", lambda: relu_backward_with_bias_backward_half_mask(
+                    p["o16"], p["dh"], p["gin"], self.dbias, R, F))]
 
     def step(self, k):
         for _, fn in self.ops(k):

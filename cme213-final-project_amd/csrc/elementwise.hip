@@ -384,6 +384,84 @@ struct GeluBwdBiasOp {  // gin = g * gelu'(in + bias)
     }
 };
 
+// ----- 16-bit storage variants (the reference's fp16 storage path,
+// activations.cu:199-217,285-347, plus bf16) --------------------------------
+
+template <int W, Fmt16 T>
+struct BiasRelu16Op {  // out16 = to16(max(in + bias, 0))
+    const float* in;
+    uint16_t* out;
+    struct In {
+        fvec<W> x;
+        __device__ void consume() const { mi::consume(x); }
+    };
+    __device__ In load(size_t i) const { return {sload<W>(in, i)}; }
+    __device__ fvec<W> apply(size_t i, const In& v, const fvec<W>& b, bool store = true) const {
+        fvec<W> o;
+#pragma unroll
+        for (int e = 0; e < W; ++e) {
+            const float t = v.x.v[e] + b.v[e];
+            o.v[e] = (t > 0.0f) ? t : 0.0f;
+        }
+        if (store) store16<W, T>(out, i, o);
+        return o;
+    }
+};
+
+template <int W, Fmt16 T>
+struct BiasGelu16Op {  // out16 = to16(gelu(in + bias))
+    const float* in;
+    uint16_t* out;
+    struct In {
+        fvec<W> x;
+        __device__ void consume() const { mi::consume(x); }
+    };
+    __device__ In load(size_t i) const { return {sload<W>(in, i)}; }
+    __device__ fvec<W> apply(size_t i, const In& v, const fvec<W>& b, bool store = true) const {
+        fvec<W> o;
+#pragma unroll
+        for (int e = 0; e < W; ++e) o.v[e] = gelu_fwd(v.x.v[e] + b.v[e]);
+        if (store) store16<W, T>(out, i, o);
+        return o;
+    }
+};
+
+template <int W, Fmt16 T>
+struct ReluBwdMask16Op {  // gin = from16(mask) > 0 ? g : 0
+    const uint16_t* mask;
+    const float* g;
+    float* gin;
+    struct In {
+        fvec<W> m, g;
+        __device__ void consume() const {
+            mi::consume(m);
+            mi::consume(g);
+        }
+    };
+    __device__ In load(size_t i) const { return {load16<W, T>(mask, i), sload<W>(g, i)}; }
+    __device__ fvec<W> apply(size_t i, const In& v, const fvec<W>&, bool store = true) const {
+        fvec<W> o;
+#pragma unroll
+        for (int e = 0; e < W; ++e) o.v[e] = (v.m.v[e] > 0.0f) ? v.g.v[e] : 0.0f;
+        if (store) sstore<W>(gin, i, o);
+        return o;
+    }
+};
+
+template <int W, Fmt16 T>
+struct To16Op {
+    const float* in;
+    uint16_t* out;
+    __device__ void operator()(size_t i) const { store16<W, T>(out, i, sload<W>(in, i)); }
+};
+
+template <int W, Fmt16 T>
+struct From16Op {
+    const uint16_t* in;
+    float* out;
+    __device__ void operator()(size_t i) const { sstore<W>(out, i, load16<W, T>(in, i)); }
+};
+
 int check_shape(const char* name, int rows, int cols) {
     if (rows < 0 || cols <= 0)
         return set_error(MI_ERR_INVALID_ARG, "%s: invalid shape rows=%d cols=%d", name, rows,
@@ -701,6 +779,117 @@ int mi_gelu_backward_with_bias_backward(const float* in, const float* bias,
                                         dbias, rows, cols, to_stream(stream));
     return launch_rowtile_reduce<1>(name, GeluBwdBiasOp<1>{in, grad_out, grad_in}, bias, dbias,
                                     rows, cols, to_stream(stream));
+}
+
+}  // extern "C"
+
+// ----- 16-bit storage ---------------------------------------------------------
+
+namespace {
+
+template <Fmt16 T>
+int convert_to16(const char* name, const float* in, void* out, long long n, void* stream) {
+    if (n < 0) return set_error(MI_ERR_INVALID_ARG, "%s: n=%lld", name, n);
+    if (n == 0) return MI_OK;
+    if (!in || !out) return set_error(MI_ERR_INVALID_ARG, "%s: NULL pointer", name);
+    uint16_t* o = static_cast<uint16_t*>(out);
+    if (n % 4 == 0 && aligned16(in) && aligned8(o))
+        return launch_flat(name, To16Op<4, T>{in, o}, n / 4, to_stream(stream));
+    return launch_flat(name, To16Op<1, T>{in, o}, n, to_stream(stream));
+}
+
+template <Fmt16 T>
+int convert_from16(const char* name, const void* in, float* out, long long n, void* stream) {
+    if (n < 0) return set_error(MI_ERR_INVALID_ARG, "%s: n=%lld", name, n);
+    if (n == 0) return MI_OK;
+    if (!in || !out) return set_error(MI_ERR_INVALID_ARG, "%s: NULL pointer", name);
+    const uint16_t* i16 = static_cast<const uint16_t*>(in);
+    if (n % 4 == 0 && aligned8(i16) && aligned16(out))
+        return launch_flat(name, From16Op<4, T>{i16, out}, n / 4, to_stream(stream));
+    return launch_flat(name, From16Op<1, T>{i16, out}, n, to_stream(stream));
+}
+
+template <Fmt16 T, bool GELU>
+int bias_act_to16(const char* name, const float* in, const float* bias, void* out, int rows,
+                  int cols, void* stream) {
+    if (int rc = check_shape(name, rows, cols)) return rc;
+    if (rows == 0) return MI_OK;
+    if (!in || !bias || !out) return set_error(MI_ERR_INVALID_ARG, "%s: NULL", name);
+    uint16_t* o = static_cast<uint16_t*>(out);
+    const bool vec4 = cols % 4 == 0 && aligned16(in) && aligned16(bias) && aligned8(o);
+    if constexpr (GELU) {
+        if (vec4)
+            return launch_rowtile<4>(name, BiasGelu16Op<4, T>{in, o}, bias, rows, cols,
+                                     to_stream(stream));
+        return launch_rowtile<1>(name, BiasGelu16Op<1, T>{in, o}, bias, rows, cols,
+                                 to_stream(stream));
+    } else {
+        if (vec4)
+            return launch_rowtile<4>(name, BiasRelu16Op<4, T>{in, o}, bias, rows, cols,
+                                     to_stream(stream));
+        return launch_rowtile<1>(name, BiasRelu16Op<1, T>{in, o}, bias, rows, cols,
+                                 to_stream(stream));
+    }
+}
+
+template <Fmt16 T>
+int relu_bwd_mask16(const char* name, const void* mask, const float* grad_out, float* grad_in,
+                    float* dbias, int rows, int cols, void* stream) {
+    if (int rc = check_shape(name, rows, cols)) return rc;
+    if (rows == 0) return MI_OK;
+    if (!mask || !grad_out || !grad_in || !dbias)
+        return set_error(MI_ERR_INVALID_ARG, "%s: NULL", name);
+    const uint16_t* m = static_cast<const uint16_t*>(mask);
+    if (cols % 4 == 0 && aligned8(m) && all_aligned({grad_out, grad_in}))
+        return launch_rowtile_reduce<4>(name, ReluBwdMask16Op<4, T>{m, grad_out, grad_in},
+                                        nullptr, dbias, rows, cols, to_stream(stream));
+    return launch_rowtile_reduce<1>(name, ReluBwdMask16Op<1, T>{m, grad_out, grad_in}, nullptr,
+                                    dbias, rows, cols, to_stream(stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+int mi_float_to_half(const float* in, void* out, long long n, void* stream) {
+    return convert_to16<Fmt16::Half>("mi_float_to_half", in, out, n, stream);
+}
+
+int mi_half_to_float(const void* in, float* out, long long n, void* stream) {
+    return convert_from16<Fmt16::Half>("mi_half_to_float", in, out, n, stream);
+}
+
+int mi_float_to_bf16(const float* in, void* out, long long n, void* stream) {
+    return convert_to16<Fmt16::BF16>("mi_float_to_bf16", in, out, n, stream);
+}
+
+int mi_bf16_to_float(const void* in, float* out, long long n, void* stream) {
+    return convert_from16<Fmt16::BF16>("mi_bf16_to_float", in, out, n, stream);
+}
+
+int mi_bias_relu_forward_to_half(const float* in, const float* bias, void* out, int rows,
+                                 int cols, void* stream) {
+    return bias_act_to16<Fmt16::Half, false>("mi_bias_relu_forward_to_half", in, bias, out, rows,
+                                             cols, stream);
+}
+
+int mi_bias_gelu_forward_to_half(const float* in, const float* bias, void* out, int rows,
+                                 int cols, void* stream) {
+    return bias_act_to16<Fmt16::Half, true>("mi_bias_gelu_forward_to_half", in, bias, out, rows,
+                                            cols, stream);
+}
+
+int mi_bias_gelu_forward_to_bf16(const float* in, const float* bias, void* out, int rows,
+                                 int cols, void* stream) {
+    return bias_act_to16<Fmt16::BF16, true>("mi_bias_gelu_forward_to_bf16", in, bias, out, rows,
+                                            cols, stream);
+}
+
+int mi_relu_backward_with_bias_backward_half_mask(const void* mask, const float* grad_out,
+                                                  float* grad_in, float* dbias, int rows,
+                                                  int cols, void* stream) {
+    return relu_bwd_mask16<Fmt16::Half>("mi_relu_backward_with_bias_backward_half_mask", mask,
+                                        grad_out, grad_in, dbias, rows, cols, stream);
 }
 
 }  // extern "C"

@@ -153,3 +153,23 @@ void buffer_norm_sq_acc(const float* buf, int n, float* d_result) {
 void compute_clip_scale(const float* d_norm_sq, float* d_clip_scale, float max_norm) {
     MI_CHECK(mi_compute_clip_scale(d_norm_sq, d_clip_scale, max_norm, per_thread_stream()));
 }
+
+void relu_backward_with_bias_backward_half_mask(const __half* mask, const float* grad_out,
+                                                float* grad_in, float* dbias, int rows,
+                                                int cols) {
+    MI_CHECK(mi_relu_backward_with_bias_backward_half_mask(mask, grad_out, grad_in, dbias, rows,
+                                                           cols, per_thread_stream()));
+}
+
+void bias_relu_forward_to_half(const float* in, const float* bias, __half* out, int rows,
+                               int cols) {
+    MI_CHECK(mi_bias_relu_forward_to_half(in, bias, out, rows, cols, per_thread_stream()));
+}
+
+void float_to_half_buffer(const float* in, __half* out, int n) {
+    MI_CHECK(mi_float_to_half(in, out, n, per_thread_stream()));
+}
+
+void half_to_float_buffer(const __half* in, float* out, int n) {
+    MI_CHECK(mi_half_to_float(in, out, n, per_thread_stream()));
+}

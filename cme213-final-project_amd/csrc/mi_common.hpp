@@ -82,6 +82,66 @@ __device__ __forceinline__ void sstore(float* base, size_t vec_index, const fvec
 }
 
 // ---------------------------------------------------------------------------
+// 16-bit storage.  Half is IEEE binary16 through the hardware conversion
+// (round to nearest even, overflow to inf); BF16 keeps the upper 16 bits of
+// the fp32 pattern, rounded to nearest even, with NaN kept a quiet NaN.
+// Vectors of 4 move as one 8-byte access.
+// ---------------------------------------------------------------------------
+enum class Fmt16 { Half, BF16 };
+
+template <Fmt16 T>
+__device__ __forceinline__ uint16_t to16(float x) {
+    if constexpr (T == Fmt16::Half) {
+        return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+    } else {
+        const uint32_t u = __float_as_uint(x);
+        if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+        return static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+    }
+}
+
+template <Fmt16 T>
+__device__ __forceinline__ float from16(uint16_t h) {
+    if constexpr (T == Fmt16::Half)
+        return static_cast<float>(__builtin_bit_cast(_Float16, h));
+    else
+        return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <int W, Fmt16 T>
+__device__ __forceinline__ fvec<W> load16(const uint16_t* base, size_t vec_index) {
+    fvec<W> r;
+    if constexpr (W == 4) {
+        const u32x2 p = reinterpret_cast<const u32x2*>(base)[vec_index];
+        r.v[0] = from16<T>(static_cast<uint16_t>(p.x & 0xffffu));
+        r.v[1] = from16<T>(static_cast<uint16_t>(p.x >> 16));
+        r.v[2] = from16<T>(static_cast<uint16_t>(p.y & 0xffffu));
+        r.v[3] = from16<T>(static_cast<uint16_t>(p.y >> 16));
+    } else {
+#pragma unroll
+        for (int e = 0; e < W; ++e) r.v[e] = from16<T>(base[vec_index * W + e]);
+    }
+    return r;
+}
+
+template <int W, Fmt16 T>
+__device__ __forceinline__ void store16(uint16_t* base, size_t vec_index, const fvec<W>& x) {
+    if constexpr (W == 4) {
+        u32x2 p;
+        p.x = static_cast<uint32_t>(to16<T>(x.v[0])) | (static_cast<uint32_t>(to16<T>(x.v[1])) << 16);
+        p.y = static_cast<uint32_t>(to16<T>(x.v[2])) | (static_cast<uint32_t>(to16<T>(x.v[3])) << 16);
+        reinterpret_cast<u32x2*>(base)[vec_index] = p;
+    } else {
+#pragma unroll
+        for (int e = 0; e < W; ++e) base[vec_index * W + e] = to16<T>(x.v[e]);
+    }
+}
+
+inline bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
+
+// ---------------------------------------------------------------------------
 // Wave64 sum.  Four DPP steps reduce each 16-lane row (quad xor-1, quad
 // xor-2, half-row mirror, row mirror); the four row totals are then read
 // with v_readlane and added in a fixed order.  Every lane returns the same

@@ -29,6 +29,8 @@
 // The same kernels are reachable through the C ABI in mi_kernels.h.
 #pragma once
 
+#include <hip/hip_fp16.h>
+
 #include "mi_kernels.h"
 
 // --- LayerNorm (reference kernels.h:53-76) ---------------------------------
@@ -87,6 +89,15 @@ void bias_gelu_forward(const float* in, const float* bias, float* out,
 void gelu_backward_with_bias_backward(const float* in, const float* bias,
                                       const float* grad_out, float* grad_in,
                                       float* dbias, int rows, int cols);
+
+// --- fp16 activation storage (reference kernels.h:84-86,108-109,115-116) ----
+void relu_backward_with_bias_backward_half_mask(const __half* mask, const float* grad_out,
+                                                float* grad_in, float* dbias, int rows,
+                                                int cols);
+void bias_relu_forward_to_half(const float* in, const float* bias, __half* out, int rows,
+                               int cols);
+void float_to_half_buffer(const float* in, __half* out, int n);
+void half_to_float_buffer(const __half* in, float* out, int n);
 
 // --- optimizer helpers (reference kernels.h:113-120) ------------------------
 void scale_buffer(float* buf, float scale, int n);

@@ -250,6 +250,44 @@ int mi_adam_update(float* param, const float* grad, float* m, float* v, long lon
 /* Workspace bytes mi_buffer_norm_sq_acc / mi_adam_update need for n floats. */
 size_t mi_norm_sq_workspace(long long n);
 
+/* ----- 16-bit activation storage ----------------------------------------- */
+/* Half buffers hold IEEE binary16 values, bf16 buffers the upper 16 bits of
+ * fp32; both are passed as void* (2 bytes per element).  Conversions round
+ * to nearest even. */
+
+/* out16[i] = half(in[i]).  Replaces float_to_half_buffer (kernels.h:115,
+ * FINAL_CLEAN_CODE/src/kernels/activations.cu:325-329,337-341). */
+int mi_float_to_half(const float* in, void* out16, long long n, void* stream);
+
+/* out[i] = float(in16[i]).  Replaces half_to_float_buffer (kernels.h:116,
+ * activations.cu:331-335,343-347). */
+int mi_half_to_float(const void* in16, float* out, long long n, void* stream);
+
+/* bf16 counterparts (no reference counterpart: the bf16 storage variant of
+ * the same path). */
+int mi_float_to_bf16(const float* in, void* out16, long long n, void* stream);
+int mi_bf16_to_float(const void* in16, float* out, long long n, void* stream);
+
+/* out16 = half(max(in + bias, 0)).  Replaces bias_relu_forward_to_half
+ * (kernels.h:108-109, activations.cu:199-217). */
+int mi_bias_relu_forward_to_half(const float* in, const float* bias, void* out16, int rows,
+                                 int cols, void* stream);
+
+/* out16 = half / bf16 (gelu(in + bias)): the bias+GELU forward with 16-bit
+ * activation storage (no reference counterpart; takes the slot of
+ * bias_relu_forward_to_half for the GELU path). */
+int mi_bias_gelu_forward_to_half(const float* in, const float* bias, void* out16, int rows,
+                                 int cols, void* stream);
+int mi_bias_gelu_forward_to_bf16(const float* in, const float* bias, void* out16, int rows,
+                                 int cols, void* stream);
+
+/* grad_in = float(mask16) > 0 ? grad_out : 0; dbias += column sums
+ * (deterministic).  Replaces relu_backward_with_bias_backward_half_mask
+ * (kernels.h:84-86, activations.cu:285-323). */
+int mi_relu_backward_with_bias_backward_half_mask(const void* mask16, const float* grad_out,
+                                                  float* grad_in, float* dbias, int rows,
+                                                  int cols, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

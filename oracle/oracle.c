@@ -377,7 +377,11 @@ void orc_bias_gelu_forward_f64(const float* in, const float* bias, double* out,
         for (int c = 0; c < cols; ++c) {
             long i = (long)r * cols + c;
             double u = (double)in[i] + (double)bias[c];
-            out[i] = 0.5 * u * (1.0 + tanh(k0 * (u + k1 * u * u * u)));
+            /* 0.5 u (1 + tanh z) written as u / (1 + e^{-2z}): the same
+             * function without the cancellation of 1 + tanh z, which in
+             * double loses every digit below u = -7 (true values 1e-16
+             * down to the underflow limit). */
+            out[i] = u / (1.0 + exp(-2.0 * k0 * (u + k1 * u * u * u)));
         }
 }
 
@@ -609,4 +613,106 @@ void orc_adam_clipped(float* param, const float* grad, float* m, float* v, float
 void orc_adam_bias_corrections(float beta1, float beta2, int step, float* bc1, float* bc2) {
     *bc1 = 1.0f - powf(beta1, (float)step);
     *bc2 = 1.0f - powf(beta2, (float)step);
+}
+
+/* ----- 16-bit storage ------------------------------------------------------ */
+
+/* float -> IEEE binary16, round to nearest even (overflow to inf, NaN kept
+ * quiet), from the format definitions; the conversion __float2half_rn of
+ * FC/src/kernels/activations.cu:206,328 performs. */
+uint16_t orc_f2h_one(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t a = x & 0x7fffffffu;
+    if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));
+    if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520: inf */
+    if (a < 0x38800000u) {                                   /* below 2^-14 */
+        if (a < 0x33000000u) return (uint16_t)sign;           /* <= 2^-25: zero */
+        uint32_t e = a >> 23;
+        uint32_t m = (a & 0x7fffffu) | 0x800000u;
+        uint32_t shift = 126u - e;                            /* 14..24 */
+        uint32_t r = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1u);
+        uint32_t half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (r & 1u))) ++r;
+        return (uint16_t)(sign | r);
+    }
+    uint32_t r = ((((a >> 23) - 127u + 15u)) << 10) | ((a & 0x7fffffu) >> 13);
+    uint32_t rem = a & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) ++r;
+    return (uint16_t)(sign | r);
+}
+
+float orc_h2f_one(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu, x;
+    if (e == 0) {
+        float v = (float)m * 5.9604644775390625e-8f; /* m * 2^-24, exact */
+        memcpy(&x, &v, 4);
+        x |= sign;
+    } else if (e == 31) {
+        x = sign | 0x7f800000u | (m << 13);
+    } else {
+        x = sign | ((e - 15u + 127u) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+/* float -> bf16: upper 16 bits, round to nearest even; NaN kept quiet. */
+uint16_t orc_f2bf_one(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+float orc_bf2f_one(uint16_t h) {
+    uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+void orc_float_to_half(const float* in, uint16_t* out, long n) {
+    for (long i = 0; i < n; ++i) out[i] = orc_f2h_one(in[i]);
+}
+void orc_half_to_float(const uint16_t* in, float* out, long n) {
+    for (long i = 0; i < n; ++i) out[i] = orc_h2f_one(in[i]);
+}
+void orc_float_to_bf16(const float* in, uint16_t* out, long n) {
+    for (long i = 0; i < n; ++i) out[i] = orc_f2bf_one(in[i]);
+}
+void orc_bf16_to_float(const uint16_t* in, float* out, long n) {
+    for (long i = 0; i < n; ++i) out[i] = orc_bf2f_one(in[i]);
+}
+
+/* bias_relu_to_half_kernel, FC/src/kernels/activations.cu:199-207. */
+void orc_bias_relu_forward_to_half(const float* in, const float* bias, uint16_t* out,
+                                   int rows, int cols) {
+    for (long idx = 0; idx < (long)rows * cols; ++idx) {
+        float val = in[idx] + bias[idx % cols];
+        val = (val > 0.0f) ? val : 0.0f;
+        out[idx] = orc_f2h_one(val);
+    }
+}
+
+/* fused_relu_backward_bias_backward_half_mask_kernel
+ * (FC/src/kernels/activations.cu:285-311) with the column sums sequential:
+ * grad_in = half2float(mask) > 0 ? grad_out : 0; dbias += column sums. */
+void orc_relu_backward_with_bias_backward_half_mask(const uint16_t* mask,
+                                                    const float* grad_out, float* grad_in,
+                                                    float* dbias, int rows, int cols) {
+    for (int c = 0; c < cols; ++c) {
+        float sum = 0.0f;
+        for (int r = 0; r < rows; ++r) {
+            long idx = (long)r * cols + c;
+            float g = (orc_h2f_one(mask[idx]) > 0.0f) ? grad_out[idx] : 0.0f;
+            grad_in[idx] = g;
+            sum += g;
+        }
+        dbias[c] += sum;
+    }
 }

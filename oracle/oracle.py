@@ -71,6 +71,10 @@ def lib():
             "orc_adam_clipped": [P, P, P, P, c_float, c_float, c_float, c_float, c_float,
                                  c_float, c_float, c_float, c_long],
             "orc_adam_bias_corrections": [c_float, c_float, c_int, P, P],
+            "orc_float_to_half": [P, P, c_long], "orc_half_to_float": [P, P, c_long],
+            "orc_float_to_bf16": [P, P, c_long], "orc_bf16_to_float": [P, P, c_long],
+            "orc_bias_relu_forward_to_half": [P, P, P, c_int, c_int],
+            "orc_relu_backward_with_bias_backward_half_mask": [P, P, P, P, c_int, c_int],
         }
         restypes = {"orc_get_threads": c_int, "orc_cross_entropy_cpu": c_float,
                     "orc_loss_mean": c_float, "orc_sumsq_f64": c_double,
@@ -417,3 +421,49 @@ def adam_bias_corrections(beta1, beta2, step):
     b1, b2 = ctypes.c_float(0), ctypes.c_float(0)
     lib().orc_adam_bias_corrections(beta1, beta2, step, ctypes.byref(b1), ctypes.byref(b2))
     return b1.value, b2.value
+
+
+# ----- 16-bit storage ----------------------------------------------------------
+
+def float_to_half(x):
+    x = f32(x)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_float_to_half(_p(x), _p(out), x.size)
+    return out
+
+
+def half_to_float(h):
+    h = _c(h, np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().orc_half_to_float(_p(h), _p(out), h.size)
+    return out
+
+
+def float_to_bf16(x):
+    x = f32(x)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_float_to_bf16(_p(x), _p(out), x.size)
+    return out
+
+
+def bf16_to_float(h):
+    h = _c(h, np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().orc_bf16_to_float(_p(h), _p(out), h.size)
+    return out
+
+
+def bias_relu_forward_to_half(x, bias):
+    x, bias = f32(x), f32(bias)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_bias_relu_forward_to_half(_p(x), _p(bias), _p(out), x.shape[0], x.shape[1])
+    return out
+
+
+def relu_backward_with_bias_backward_half_mask(mask16, g, dbias=None):
+    mask16, g = _c(mask16, np.uint16), f32(g)
+    gin = np.empty_like(g)
+    db = np.zeros(g.shape[1], np.float32) if dbias is None else f32(dbias).copy()
+    lib().orc_relu_backward_with_bias_backward_half_mask(_p(mask16), _p(g), _p(gin), _p(db),
+                                                         g.shape[0], g.shape[1])
+    return gin, db

@@ -261,8 +261,9 @@ def test_gelu_against_torch_golden():
     x = u.reshape(1, -1)
     zero_bias = np.zeros(u.size, np.float32)
     y64 = O.bias_gelu_forward_f64(x, zero_bias)[0]
-    # Both float64 evaluations of 1 + tanh(z) cancel for u < -10 (true value
-    # < 1e-40); they agree to 1e-15 absolute there.
+    # torch evaluates 1 + tanh(z), which cancels in double below u = -7; the
+    # oracle's logistic form does not, and the two agree to 1e-15 absolute
+    # there (the golden values are the inexact ones).
     np.testing.assert_allclose(y64, d["y"], rtol=1e-13, atol=1e-15)
     gin64, _ = O.gelu_backward_with_bias_backward_f64(x, zero_bias, g.reshape(1, -1))
     np.testing.assert_allclose(gin64[0], d["gin"], rtol=1e-12, atol=1e-14)
@@ -599,3 +600,61 @@ def test_scale_and_sumsq():
     x = r.standard_normal(1001).astype(np.float32)
     assert np.array_equal(O.scale_buffer(x, 0.25).view(np.uint32), (x * np.float32(0.25)).view(np.uint32))
     assert abs(O.sumsq_f64(x) - float((x.astype(np.float64) ** 2).sum())) < 1e-9
+
+
+# ----------------------------------------------------------------------------
+# 16-bit storage
+# ----------------------------------------------------------------------------
+
+def _f32_specials_and_random():
+    bits = np.array([0x00000000, 0x80000000, 0x7f800000, 0xff800000, 0x7fc00000, 0x7f800001,
+                     0x33000000, 0x33000001, 0x33800000, 0x387fc000, 0x387fe000, 0x387ff000,
+                     0x38800000, 0x477fe000, 0x477fefff, 0x477ff000, 0x477ff001, 0x7f7fffff,
+                     0x3f800000, 0x3f801000, 0x3f802000, 0x3f803000, 0x3f808000, 0x00000001,
+                     0x007fffff, 0x3effffff, 0xc0490fdb], np.uint32)
+    r = rng(51)
+    rand_bits = r.integers(0, 2 ** 32, 200000, dtype=np.uint64).astype(np.uint32)
+    ranged = (r.standard_normal(100000) * np.exp(r.uniform(-30, 15, 100000))).astype(np.float32)
+    return np.concatenate([bits.view(np.float32), rand_bits.view(np.float32), ranged])
+
+
+def test_half_conversion_matches_numpy():
+    # numpy's float32 -> float16 cast (round to nearest even) is independent
+    x = _f32_specials_and_random()
+    h = O.float_to_half(x)
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = x.astype(np.float16).view(np.uint16)
+    nan = np.isnan(x)
+    assert np.array_equal(h[~nan], ref[~nan])
+    assert np.isnan(O.half_to_float(h[nan])).all()
+    # every half value converts back exactly
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f = O.half_to_float(allh)
+    fin = ~np.isnan(allh.view(np.float16))
+    assert np.array_equal(f[fin].view(np.uint32), allh.view(np.float16)[fin].astype(np.float32).view(np.uint32))
+    assert np.array_equal(O.float_to_half(f[fin]), allh[fin])
+
+
+def test_bf16_conversion_matches_torch():
+    import torch
+    x = _f32_specials_and_random()
+    b = O.float_to_bf16(x)
+    ref = torch.from_numpy(x.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    nan = np.isnan(x)
+    assert np.array_equal(b[~nan], ref[~nan])
+    assert np.isnan(O.bf16_to_float(b[nan])).all()
+    back = O.bf16_to_float(b[~nan])
+    assert np.array_equal(back, torch.from_numpy(ref[~nan].view(np.int16).copy()).view(
+        torch.bfloat16).float().numpy())
+
+
+def test_fp16_storage_ops():
+    r = rng(53)
+    x = (2 * r.standard_normal((37, 129))).astype(np.float32)
+    b = (0.1 * r.standard_normal(129)).astype(np.float32)
+    h = O.bias_relu_forward_to_half(x, b)
+    assert np.array_equal(h, np.maximum(x + b, np.float32(0)).astype(np.float16).view(np.uint16))
+    g = r.standard_normal((37, 129)).astype(np.float32)
+    gin, db = O.relu_backward_with_bias_backward_half_mask(h, g)
+    gin2, db2 = O.relu_backward_with_bias_backward(O.half_to_float(h), g)
+    assert np.array_equal(gin, gin2) and np.array_equal(db, db2)
