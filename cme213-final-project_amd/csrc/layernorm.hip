@@ -30,7 +30,10 @@ namespace mi {
 
 namespace {
 
-constexpr int kFwdWaves = 4;      // rows (waves) per forward workgroup
+#ifndef MI_LN_FWD_WAVES
+#define MI_LN_FWD_WAVES 4
+#endif
+constexpr int kFwdWaves = MI_LN_FWD_WAVES;  // waves per forward workgroup
 #ifndef MI_LN_BWD_WAVES
 #define MI_LN_BWD_WAVES 8
 #endif
