@@ -58,7 +58,7 @@ __global__ __launch_bounds__(kRowWaves * kWave) void emb_fwd_kernel(
 #pragma unroll
             for (int e = 0; e < W; ++e) v.v[e] = v.v[e] + q.v[e];
         }
-        vstore<W>(dst, j, v);
+        sstore<W>(dst, j, v);  // streamed out: measured 20.9 -> 16.0 us at config 2
     }
 }
 
@@ -261,9 +261,21 @@ __global__ __launch_bounds__(kRowWaves * kWave) void emb_bwd_accum_kernel(
     const int lane = threadIdx.x & (kWave - 1);
     const int s = blockIdx.x * kRowWaves + static_cast<int>(threadIdx.x / kWave);
     if (s >= n) return;
-    const unsigned key = keys[s];
-    if (key == kSentinel) return;
-    if (s > 0 && keys[s - 1] == key) return;
+    // One load covers the previous position (lane 0) and the first 63
+    // positions from s (lanes 1..63): the run-start test, the run's extent
+    // in this window and its grad row indices all come from one round trip,
+    // and the table row and grad rows are then requested together.
+    constexpr unsigned kNoKey = 0xFFFFFFFEu;  // no key takes this value
+    const int e0 = s - 1 + lane;
+    const bool in = e0 >= 0 && e0 < n;
+    const unsigned kk = in ? keys[e0] : kNoKey;
+    const int vv = (in && lane > 0) ? vals[e0] : 0;
+    const unsigned key = __shfl(kk, 1, kWave);
+    if (key == kSentinel || __shfl(kk, 0, kWave) == key) return;  // wave-uniform
+    // Run length within the window: trailing set bits of the match mask of
+    // positions s, s+1, ... (lanes 1..63).
+    const unsigned long long m0 = __ballot(lane > 0 && kk == key) >> 1;
+    const int cnt0 = (~m0 == 0ull) ? 64 : (__ffsll(static_cast<unsigned long long>(~m0)) - 1);
     const int nv = dim / W;
     float* trow = table + static_cast<size_t>(key) * dim;
     for (int c0 = 0; c0 < nv; c0 += NCH * kWave) {
@@ -273,22 +285,16 @@ __global__ __launch_bounds__(kRowWaves * kWave) void emb_bwd_accum_kernel(
             const int j = c0 + lane + k * kWave;
             acc[k] = j < nv ? vload<W>(trow, j) : vzero<W>();
         }
-        // Walk the run 64 positions at a time; a chunk's keys tell where the
-        // run ends, its values which grad rows to add.
-        for (int b0 = s;; b0 += kWave) {
-            const int e = b0 + lane;
-            const bool same = e < n && keys[e] == key;
-            const int my_i = same ? vals[e] : 0;
-            const unsigned long long m = __ballot(same);
-            // the run is contiguous from b0, so its length in this chunk is
-            // the number of trailing set bits
-            const int cnt = (~m == 0ull) ? kWave : (__ffsll(static_cast<unsigned long long>(~m)) - 1);
+        // Adds `cnt` grad rows whose indices sit in lanes off, off+1, ... of
+        // `idx`, in order, kAccBatch rows per group of loads.
+        auto add_rows = [&](int idx, int off, int cnt) {
             int q = 0;
             for (; q + kAccBatch <= cnt; q += kAccBatch) {
                 fvec<W> v[kAccBatch][NCH];
 #pragma unroll
                 for (int u = 0; u < kAccBatch; ++u) {
-                    const float* grow = g + static_cast<size_t>(__shfl(my_i, q + u, kWave)) * dim;
+                    const float* grow =
+                        g + static_cast<size_t>(__shfl(idx, off + q + u, kWave)) * dim;
 #pragma unroll
                     for (int k = 0; k < NCH; ++k) {
                         const int j = c0 + lane + k * kWave;
@@ -303,7 +309,7 @@ __global__ __launch_bounds__(kRowWaves * kWave) void emb_bwd_accum_kernel(
                         for (int x = 0; x < W; ++x) acc[k].v[x] = acc[k].v[x] + v[u][k].v[x];
             }
             for (; q < cnt; ++q) {
-                const float* grow = g + static_cast<size_t>(__shfl(my_i, q, kWave)) * dim;
+                const float* grow = g + static_cast<size_t>(__shfl(idx, off + q, kWave)) * dim;
 #pragma unroll
                 for (int k = 0; k < NCH; ++k) {
                     const int j = c0 + lane + k * kWave;
@@ -314,7 +320,21 @@ __global__ __launch_bounds__(kRowWaves * kWave) void emb_bwd_accum_kernel(
                     }
                 }
             }
-            if (cnt < kWave) break;
+        };
+        const int first = cnt0 < 63 ? cnt0 : 63;
+        add_rows(vv, 1, first);
+        if (cnt0 >= 63) {
+            // Long runs: continue 64 positions at a time after the window.
+            for (int b0 = s + 63;; b0 += kWave) {
+                const int e = b0 + lane;
+                const bool same = e < n && keys[e] == key;
+                const int my_i = same ? vals[e] : 0;
+                const unsigned long long m = __ballot(same);
+                const int cnt =
+                    (~m == 0ull) ? kWave : (__ffsll(static_cast<unsigned long long>(~m)) - 1);
+                add_rows(my_i, 0, cnt);
+                if (cnt < kWave) break;
+            }
         }
 #pragma unroll
         for (int k = 0; k < NCH; ++k) {

@@ -58,6 +58,11 @@ def test_reference_embedding_test_case(dev):
     (1000, 100, 3, 333, 1000),       # D % 4 != 0, ragged tile
     (7, 64, 2, 4, 7),                # tiny vocabulary, long runs
     (70000, 16, 1, 1, 70000),        # one token, 17-bit keys
+    # more than 16384 tokens: the multi-kernel radix sort (tiles across
+    # workgroups) instead of the single-workgroup LDS sort
+    (50257, 64, 33, 1000, 50257),
+    (300, 32, 1, 16385, 300),        # one past the single-workgroup limit, long runs
+    (70000, 16, 2, 9000, 0),         # trusted ids, 32-bit keys, 18000 tokens
 ])
 def test_embedding_forward_backward(dev, V, D, B, T, vocab_arg):
     note(f"embedding V={V} D={D} B={B} T={T} vocab_arg={vocab_arg}")
