@@ -41,28 +41,23 @@ constexpr int kBwdWaves = MI_LN_BWD_WAVES;  // waves per backward workgroup
 constexpr int kBlockThreads = 256;  // generic block-per-row kernels
 
 // ---------------------------------------------------------------------------
-// Forward: each wave normalises kFwdRows consecutive rows, held in registers.
-// All loads of those rows are issued first (column indices clamped into the
-// row, masked slots zeroed afterwards), then each row is reduced and written.
+// Forward: each wave normalises R consecutive rows, held in registers.  All
+// loads of those rows are issued first (column indices clamped into the row,
+// masked slots zeroed afterwards), then each row is reduced and written.
 // ---------------------------------------------------------------------------
-#ifndef MI_LN_FWD_ROWS
-#define MI_LN_FWD_ROWS 2
-#endif
-constexpr int kFwdRows = MI_LN_FWD_ROWS;
-
-template <int W, int N, bool SAVE, bool RESID>
+template <int W, int N, int R, bool SAVE, bool RESID>
 __global__ __launch_bounds__(kFwdWaves * kWave) void ln_fwd_wave_kernel(
     const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ gamma,
     const float* __restrict__ beta, float* __restrict__ resid_out, float* __restrict__ out,
     float* __restrict__ mean_out, float* __restrict__ rstd_out, int rows, int cols, float eps) {
     const int lane = threadIdx.x & (kWave - 1);
-    const int row0 = (blockIdx.x * kFwdWaves + static_cast<int>(threadIdx.x / kWave)) * kFwdRows;
+    const int row0 = (blockIdx.x * kFwdWaves + static_cast<int>(threadIdx.x / kWave)) * R;
     if (row0 >= rows) return;  // wave-uniform
     const int nv = cols / W;
 
-    fvec<W> v[kFwdRows][N];
+    fvec<W> v[R][N];
 #pragma unroll
-    for (int r = 0; r < kFwdRows; ++r) {
+    for (int r = 0; r < R; ++r) {
         const int rr = row0 + r < rows ? row0 + r : rows - 1;
         const size_t base = static_cast<size_t>(rr) * cols;
 #pragma unroll
@@ -79,7 +74,7 @@ __global__ __launch_bounds__(kFwdWaves * kWave) void ln_fwd_wave_kernel(
     }
 
 #pragma unroll
-    for (int r = 0; r < kFwdRows; ++r) {
+    for (int r = 0; r < R; ++r) {
         const int row = row0 + r;
         if (row >= rows) break;  // wave-uniform
         const size_t base = static_cast<size_t>(row) * cols;
@@ -220,14 +215,13 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void ln_bwd_group_kernel(
     const int stride = gridDim.x * GPB;
     // One row's inputs.  Every load is unconditional (row and column indices
     // are clamped into the tensor, masked slots are zeroed after the load),
-    // so the loads carry no branches.  Loading the next row while the
-    // current one is processed measured 0.5 us slower at [8192, 768].
+    // so the loads carry no branches.
     struct RowIn {
         fvec<W> go[N], xv[N];
         float mu, is;
     };
-    auto load_row = [&](int row, RowIn& d) {
-        const int rr = row < rows ? row : rows - 1;
+    auto load_row = [&](long long row, RowIn& d) {
+        const int rr = row < rows ? static_cast<int>(row) : rows - 1;
         const size_t off = static_cast<size_t>(rr) * cols;
 #pragma unroll
         for (int k = 0; k < N; ++k) {
@@ -239,7 +233,7 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void ln_bwd_group_kernel(
         d.mu = mean[rr];
         d.is = rstd[rr];
     };
-    auto process = [&](const RowIn& cur, int row, int parity) {
+    auto process = [&](const RowIn& cur, long long row, int parity) {
         const bool valid = row < rows;
         const size_t off = static_cast<size_t>(valid ? row : 0) * cols;
         const float mu = cur.mu;
@@ -320,13 +314,24 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void ln_bwd_group_kernel(
 
     // The trip count is uniform across the workgroup (groups past the last
     // row process a masked row), so the barriers in process() are reached by
-    // every wave.
+    // every wave.  RF rows are loaded before the first is processed; rows
+    // are still processed, and summed into ag/ab, in increasing order.  With
+    // one wave per row (G = 1) one row in flight measured fastest ([8192,
+    // 768]: 2 or 4 rows were 0.4-0.5 us slower); with several waves per row
+    // two rows in flight were faster ([8192, 1600]: 34.0 against 36.7 us;
+    // [32768, 1600]: 109.5 against 123.6 us).
+    constexpr int RF = G > 1 ? 2 : 1;
     const int first = blockIdx.x * GPB;
     const int iters = first < rows ? (rows - first + stride - 1) / stride : 0;
-    RowIn cur;
-    for (int i = 0, row = first + grp; i < iters; ++i, row += stride) {
-        load_row(row, cur);
-        process(cur, row, i & 1);
+    // Row numbers are 64-bit: with rows near INT_MAX, row + r * stride may
+    // exceed the int range for the masked tail.
+    long long row = first + grp;
+    for (int i = 0; i < iters; i += RF, row += static_cast<long long>(RF) * stride) {
+        RowIn cur[RF];
+#pragma unroll
+        for (int r = 0; r < RF; ++r) load_row(row + r * stride, cur[r]);
+#pragma unroll
+        for (int r = 0; r < RF; ++r) process(cur[r], row + r * stride, (i + r) & 1);
     }
 
     // Combine the GPB groups' running sums: a fixed binary tree through LDS.
@@ -426,15 +431,29 @@ int pick_n(int need) {
     return 0;
 }
 
-template <int W, bool SAVE, bool RESID>
-void launch_fwd_wave(int n, dim3 grid, hipStream_t st, const float* a, const float* b,
-                     const float* gamma, const float* beta, float* ro, float* out, float* mo,
-                     float* so, int rows, int cols, float eps) {
+// Rows per wave of the forward kernel, from a sweep over rows x {768, 1600}
+// on MI355X.  Two rows per wave measured faster for 6M-16M elements when
+// there are at least 6144 rows ([8192, 768]: 9.2 against 9.6 us; [6144,
+// 1600]: 14.6 against 16.5 us; [8192, 1600]: 18.4 against 21.2 us), one row
+// per wave elsewhere ([4096, 768]: 5.5 against 6.8 us; [4096, 1600]: 9.8
+// against 10.6 us; [12288, 1600]: 29.5 against 32.0 us; [65536, 768]: 67.4
+// against 70.5 us).
+int fwd_rows_per_wave(int rows, int cols) {
+    const long long elems = static_cast<long long>(rows) * cols;
+    return (rows >= 6144 && elems >= (6ll << 20) && elems <= (16ll << 20)) ? 2 : 1;
+}
+
+template <int W, int R, bool SAVE, bool RESID>
+void launch_fwd_wave(int n, hipStream_t st, const float* a, const float* b, const float* gamma,
+                     const float* beta, float* ro, float* out, float* mo, float* so, int rows,
+                     int cols, float eps) {
+    const int waves = (rows + R - 1) / R;
+    const dim3 grid((waves + kFwdWaves - 1) / kFwdWaves);
     const dim3 block(kFwdWaves * kWave);
-#define MI_LN_FWD_CASE(NN)                                                                  \
-    case NN:                                                                                \
-        hipLaunchKernelGGL((ln_fwd_wave_kernel<W, NN, SAVE, RESID>), grid, block, 0, st, a, \
-                           b, gamma, beta, ro, out, mo, so, rows, cols, eps);               \
+#define MI_LN_FWD_CASE(NN)                                                                     \
+    case NN:                                                                                   \
+        hipLaunchKernelGGL((ln_fwd_wave_kernel<W, NN, R, SAVE, RESID>), grid, block, 0, st, a, \
+                           b, gamma, beta, ro, out, mo, so, rows, cols, eps);                  \
         break;
     switch (n) {
         MI_LN_FWD_CASE(1)
@@ -467,14 +486,19 @@ int ln_forward_impl(const char* name, const float* a, const float* b, const floa
     const int need = (cols / W + kWave - 1) / kWave;
     const int n = pick_n(need);
     if (n != 0) {
-        const int waves = (rows + kFwdRows - 1) / kFwdRows;
-        const dim3 grid((waves + kFwdWaves - 1) / kFwdWaves);
-        if (vec4)
-            launch_fwd_wave<4, SAVE, RESID>(n, grid, st, a, b, gamma, beta, ro, out, mo, so, rows,
-                                            cols, eps);
+        const bool two = fwd_rows_per_wave(rows, cols) == 2;
+        if (vec4 && two)
+            launch_fwd_wave<4, 2, SAVE, RESID>(n, st, a, b, gamma, beta, ro, out, mo, so, rows,
+                                               cols, eps);
+        else if (vec4)
+            launch_fwd_wave<4, 1, SAVE, RESID>(n, st, a, b, gamma, beta, ro, out, mo, so, rows,
+                                               cols, eps);
+        else if (two)
+            launch_fwd_wave<1, 2, SAVE, RESID>(n, st, a, b, gamma, beta, ro, out, mo, so, rows,
+                                               cols, eps);
         else
-            launch_fwd_wave<1, SAVE, RESID>(n, grid, st, a, b, gamma, beta, ro, out, mo, so, rows,
-                                            cols, eps);
+            launch_fwd_wave<1, 1, SAVE, RESID>(n, st, a, b, gamma, beta, ro, out, mo, so, rows,
+                                               cols, eps);
     } else {
         hipLaunchKernelGGL((ln_fwd_block_kernel<SAVE, RESID>), dim3(rows), dim3(kBlockThreads), 0,
                            st, a, b, gamma, beta, ro, out, mo, so, rows, cols, eps);

@@ -14,11 +14,14 @@ pytestmark = pytest.mark.gpu
 
 # (rows, cols, seed): config 0, the metric's LN, config 4 (C=1600 tail and
 # the wide sweep), the reference test shape, scalar / odd widths, widths past
-# the register-resident templates.
+# the register-resident templates.  Tensors of 6M-16M elements with at least
+# 6144 rows take the two-rows-per-wave forward; (6161, 1022) covers it with
+# scalar loads and an odd row count (the last wave has one row).
 SHAPES = [
     (4096, 768, 20260),
     (8192, 768, 20261),
     (4096, 1600, 20264),
+    (6161, 1022, 20265),
     (2048, 128, 42),
     (37, 33, 1),
     (1, 768, 2),
@@ -68,7 +71,7 @@ def test_layernorm_forward_backward(dev, rows, cols, seed):
 
 
 @pytest.mark.parametrize("rows,cols,seed", [(4096, 768, 11), (1024, 1600, 12), (33, 65, 13),
-                                            (64, 4096, 14)])
+                                            (64, 4096, 14), (6145, 1600, 15)])
 def test_residual_layernorm_and_backward_residual(dev, rows, cols, seed):
     note(f"residual layernorm rows={rows} cols={cols}")
     x, gamma, beta, g = ln_inputs(rows, cols, seed)
