@@ -17,13 +17,13 @@
  *
  * All pointers are device pointers owned by the caller, fp32 row-major
  * contiguous (ids int32).  Calls are asynchronous on `stream` and perform no
- * host synchronisation.  The column reductions (dgamma/dbeta/dbias, the
- * embedding gradients) are deterministic: two-pass, no float atomics, so
- * repeated calls on identical inputs give identical bits.  Those entry points
- * use a library-owned device workspace; it is allocated on first use (or by
- * mi_workspace_reserve) and may not grow while the stream is being captured
- * into a graph.  Calls that share the workspace must not run concurrently on
- * different streams of the same device.
+ * host synchronisation.  The column reductions (dgamma/dbeta/dbias) and the
+ * embedding gradients are deterministic (no float atomics), so repeated calls
+ * on identical inputs give identical bits.  The column reductions are
+ * two-pass and use a library-owned device workspace; it is allocated on first
+ * use (or by mi_workspace_reserve) and may not grow while the stream is being
+ * captured into a graph.  Calls that share the workspace must not run
+ * concurrently on different streams of the same device.
  */
 #ifndef MI_KERNELS_H
 #define MI_KERNELS_H
@@ -55,7 +55,8 @@ int mi_device_sync(void);
  * before graph capture).  mi_workspace_bytes() reports its current size. */
 int mi_workspace_reserve(size_t bytes);
 size_t mi_workspace_bytes(void);
-/* Workspace an entry point needs for the given shape (bytes). */
+/* Workspace an entry point needs for the given shape (bytes).  The token
+ * embedding backward needs none: mi_embedding_backward_workspace returns 0. */
 size_t mi_layernorm_backward_workspace(int rows, int cols);
 size_t mi_bias_backward_workspace(int rows, int cols);
 size_t mi_embedding_backward_workspace(int batch_seq);
@@ -160,10 +161,10 @@ int mi_embedding_forward(const float* table, const int* tokens, float* out,
                          int batch_seq, int dim, int vocab, void* stream);
 
 /* grad_table[tokens[i], :] += grad_out[i, :], each table row accumulated in
- * increasing i (deterministic, same order as the CPU loop).  vocab > 0
- * skips ids outside [0, vocab) and sorts only the bits vocab needs; vocab
- * <= 0 trusts the ids.  Replaces embedding_backward (kernels.h:133-134,
- * embedding.cu:33-40). */
+ * increasing i (deterministic, same order as the CPU loop); one kernel, no
+ * workspace.  vocab > 0 skips ids outside [0, vocab); vocab <= 0 trusts the
+ * ids (negative ids are skipped).  Replaces embedding_backward
+ * (kernels.h:133-134, embedding.cu:33-40). */
 int mi_embedding_backward(const float* grad_out, const int* tokens, float* grad_table,
                           int batch_seq, int dim, int vocab, void* stream);
 

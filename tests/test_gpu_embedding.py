@@ -54,15 +54,16 @@ def test_reference_embedding_test_case(dev):
 
 @pytest.mark.parametrize("V,D,B,T,vocab_arg", [
     (50257, 768, 16, 1024, 50257),
-    (50257, 768, 16, 1024, 0),       # ids trusted: full 32-bit key sort
-    (1000, 100, 3, 333, 1000),       # D % 4 != 0, ragged tile
-    (7, 64, 2, 4, 7),                # tiny vocabulary, long runs
-    (70000, 16, 1, 1, 70000),        # one token, 17-bit keys
-    # more than 16384 tokens: the multi-kernel radix sort (tiles across
-    # workgroups) instead of the single-workgroup LDS sort
+    (50257, 768, 16, 1024, 0),       # ids trusted (no vocabulary bound)
+    (1000, 100, 3, 333, 1000),       # D % 4 != 0, ragged last id group
+    (7, 64, 2, 4, 7),                # tiny vocabulary, one owning workgroup, long runs
+    (70000, 16, 1, 1, 70000),        # one token
+    # more than 16384 tokens: several passes over the ids per workgroup
     (50257, 64, 33, 1000, 50257),
-    (300, 32, 1, 16385, 300),        # one past the single-workgroup limit, long runs
-    (70000, 16, 2, 9000, 0),         # trusted ids, 32-bit keys, 18000 tokens
+    (300, 32, 1, 16385, 300),        # one token into the second pass, long runs
+    (70000, 16, 2, 9000, 0),         # trusted ids, 18000 tokens
+    (2000, 1600, 2, 500, 2000),      # GPT-2-XL width: 4 vectors per lane, 2 column chunks
+    (500, 1030, 1, 700, 500),        # scalar columns, 5 column chunks
 ])
 def test_embedding_forward_backward(dev, V, D, B, T, vocab_arg):
     note(f"embedding V={V} D={D} B={B} T={T} vocab_arg={vocab_arg}")
@@ -94,7 +95,8 @@ def test_embedding_forward_backward(dev, V, D, B, T, vocab_arg):
 def test_heavy_hitter_and_invalid_ids(dev):
     V, D, B, T = 300, 64, 4, 1100
     wte, wpe, ids, g = emb_inputs(V, D, B, T, 9)
-    ids[: 3000] = 17            # one id repeated 3000 times (runs span tiles)
+    ids[: 3000] = 17            # one id repeated 3000 times: runs of 64+ entries and
+                                # more list entries than one LDS window holds
     ids[3000:3010] = -5          # invalid ids: skipped by the bounded entry points
     ids[3010:3020] = V + 4
     BT = B * T
