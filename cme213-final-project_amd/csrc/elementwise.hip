@@ -144,7 +144,7 @@ template <class Op>
 int launch_flat(const char* name, Op op, long long nvec, hipStream_t st) {
     if (nvec <= 0) return MI_OK;
     long long grid = (nvec + kThreads - 1) / kThreads;
-    if (grid > 16384) grid = 16384;
+    if (grid > MI_FLAT_MAX_GRID) grid = MI_FLAT_MAX_GRID;
     hipLaunchKernelGGL(flat_kernel<Op>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, st,
                        op, nvec);
     return check_launch(name);

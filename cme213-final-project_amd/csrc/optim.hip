@@ -97,6 +97,13 @@ struct AdamArgs {
     float lr, beta1, beta2, eps, bc1, bc2, grad_scale;
 };
 
+// Adam: one thread per vector, up to kAdamGrid workgroups (a grid-stride
+// loop only beyond 2^25 vectors).  With seven streams per element, short
+// workgroups measured faster than long grid-stride loops at 124M
+// parameters: 630 us with 131072 workgroups against 738 us with 16384 (and
+// 799 us with 2048).
+constexpr int kAdamGrid = 131072;
+
 template <int W>
 __global__ __launch_bounds__(kOptThreads) void adam_kernel(float* __restrict__ param,
                                                            const float* __restrict__ grad,
@@ -186,7 +193,7 @@ int adam_impl(const char* name, float* param, const float* grad, float* m, float
     const bool vec4 = n % 4 == 0 && aligned16(param) && aligned16(grad) && aligned16(m) &&
                       aligned16(v);
     const long long nvec = vec4 ? n / 4 : n;
-    const dim3 grid(flat_grid(nvec, 16384));
+    const dim3 grid(flat_grid(nvec, kAdamGrid));
     if (vec4)
         hipLaunchKernelGGL(adam_kernel<4>, grid, dim3(kOptThreads), 0, st, param, grad, m, v, clip,
                            a, nvec);
