@@ -66,6 +66,7 @@ def cpu_baseline(inputs, seconds):
     times.sort()
     med = times[len(times) // 2]
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "rows_per_s": round(R / med, 1),
             "sample": f"{len(times)} full headline steps (LN [{R},{C}] fwd+bwd + bias+GELU "
                       f"[{R},{F}] fwd+bwd), median {med * 1e3:.1f} ms/step, single thread"}
 
@@ -184,6 +185,11 @@ def main():
         "config": {"workload": WORKLOADS[args.workload], "bytes_per_step": step_bytes,
                    "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2)},
     }
+    # Token rows carried through the path per second (B*T rows per step; the
+    # block sequences carry them through every layer).
+    rows = getattr(wl, "R", None) or (getattr(wl, "B", 0) * getattr(wl, "T", 0)) or None
+    if rows:
+        line["rows_per_s"] = round(rows / (ms_per_step * 1e-3), 1)
     if op_ms:
         line["breakdown_us"] = {n: round(v * 1e3, 3) for n, v in op_ms.items()}
         line["breakdown_gbs"] = {n: round(wl.bytes[n] / (op_ms[n] * 1e-3) / 1e9, 1)
