@@ -16,7 +16,13 @@
 // Every bracketed GEMM / attention step is replaced by a fixed stand-in
 // tensor that a small copy kernel writes where the GEMM would write its
 // output.  With "gelu" the bias+ReLU pair is replaced by bias_gelu_forward /
-// gelu_backward_with_bias_backward (the activation this library adds).
+// gelu_backward_with_bias_backward (the activation this library adds).  With
+// "fp16" the reference's CME213_FP16_STORAGE_ONLY path runs instead
+// (transformer.cu:293-324, 490-518): bias_relu_forward in place on
+// ff_hidden, a float_to_half_buffer / half_to_float_buffer round trip
+// through the half copy of the activation, half_to_float_buffer again at the
+// start of the FFN backward, and relu_backward_with_bias_backward_half_mask
+// with the half activation as the mask.
 //
 // Like main.cu:264-320 (CME213_USE_CUDA_GRAPH=1), three eager warm-up steps
 // run first; then zero_grad + forward + backward is captured on the
@@ -27,7 +33,7 @@
 // step are written to DIR as raw little-endian arrays for the CPU oracle
 // comparison in tests/test_gpu_transformer_nongemm.py.
 //
-// usage: transformer_nongemm DIR relu|gelu [B T D FF V]
+// usage: transformer_nongemm DIR relu|gelu|fp16 [B T D FF V]
 // exit status: 0 = ran and every replay matched, 1 = replay mismatch,
 // 2 = HIP error or bad arguments.
 #include <hip/hip_runtime.h>
@@ -113,11 +119,12 @@ static void dump(const std::string& dir, const std::string& name, const void* p,
 
 int main(int argc, char** argv) {
     if (argc < 3) {
-        std::fprintf(stderr, "usage: %s DIR relu|gelu [B T D FF V]\n", argv[0]);
+        std::fprintf(stderr, "usage: %s DIR relu|gelu|fp16 [B T D FF V]\n", argv[0]);
         return 2;
     }
     const std::string dir = argv[1];
     const bool gelu = std::strcmp(argv[2], "gelu") == 0;
+    const bool fp16 = std::strcmp(argv[2], "fp16") == 0;
     const int B = argc > 3 ? std::atoi(argv[3]) : 4;
     const int T = argc > 4 ? std::atoi(argv[4]) : 128;
     const int D = argc > 5 ? std::atoi(argv[5]) : 768;
@@ -126,7 +133,7 @@ int main(int argc, char** argv) {
     if (B <= 0 || T <= 0 || D <= 0 || FF <= 0 || V <= 0) return 2;
     const int BT = B * T;
     std::printf("transformer non-GEMM sequence: %s B=%d T=%d D=%d FF=%d V=%d\n",
-                gelu ? "gelu" : "relu", B, T, D, FF, V);
+                gelu ? "gelu" : (fp16 ? "fp16" : "relu"), B, T, D, FF, V);
 
     // Parameters (fixed) and the flat gradient buffer (zero_grad clears it
     // in one pass, transformer.cu:260-263).
@@ -179,7 +186,11 @@ int main(int argc, char** argv) {
     Buf* ln2_mean = make("ln2_mean", BT);
     Buf* ln2_inv = make("ln2_inv_std", BT);
     Buf* ff_hidden = make("ff_hidden", nF);
-    Buf* ff_act = make("ff_act", nF);
+    // fp16 storage: the activation lives in ff_hidden (in place) and in a
+    // half copy (nF halves held in a float-sized buffer).
+    Buf* ff_act = fp16 ? nullptr : make("ff_act", nF);
+    Buf* ff_relu_half = fp16 ? make("ff_relu_half", (nF + 1) / 2) : nullptr;
+    __half* act_half = fp16 ? reinterpret_cast<__half*>(ff_relu_half->d) : nullptr;
     Buf* ff_out = make("ff_out", nD);
     Buf* residual2 = make("residual2", nD);
     Buf* grad_res2 = make("grad_residual2", nD);
@@ -206,19 +217,28 @@ int main(int argc, char** argv) {
         residual_layernorm_forward_save(embedded->d, attn_proj->d, ln2_g->d, ln2_b->d,
                                         residual1->d, ln2_out->d, ln2_mean->d, ln2_inv->d, BT, D);
         gemm_standin(s_ff_hidden, ff_hidden);
-        if (gelu)
+        if (gelu) {
             bias_gelu_forward(ff_hidden->d, b1->d, ff_act->d, BT, FF);
-        else
+        } else if (fp16) {
+            bias_relu_forward(ff_hidden->d, b1->d, ff_hidden->d, BT, FF);
+            float_to_half_buffer(ff_hidden->d, act_half, static_cast<int>(nF));
+            half_to_float_buffer(act_half, ff_hidden->d, static_cast<int>(nF));
+        } else {
             bias_relu_forward(ff_hidden->d, b1->d, ff_act->d, BT, FF);
+        }
         gemm_standin(s_ff_out, ff_out);
         residual_add_with_bias(residual1->d, ff_out->d, b2->d, residual2->d, BT, D);
         // backward
         gemm_standin(s_grad_res2, grad_res2);
+        if (fp16) half_to_float_buffer(act_half, ff_hidden->d, static_cast<int>(nF));
         bias_backward(grad_res2->d, db2, BT, D);
         gemm_standin(s_grad_ff_act, grad_ff_act);
         if (gelu)
             gelu_backward_with_bias_backward(ff_hidden->d, b1->d, grad_ff_act->d,
                                              grad_ff_hidden->d, db1, BT, FF);
+        else if (fp16)
+            relu_backward_with_bias_backward_half_mask(act_half, grad_ff_act->d,
+                                                       grad_ff_hidden->d, db1, BT, FF);
         else
             relu_backward_with_bias_backward(ff_act->d, grad_ff_act->d, grad_ff_hidden->d, db1,
                                              BT, FF);

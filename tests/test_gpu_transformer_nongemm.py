@@ -11,7 +11,9 @@ Here the eager step's outputs are compared with the same sequence run
 through the CPU oracle: adds, gathers, ReLU and the embedding gradients
 bit-exact; LN outputs and statistics at the forward tolerance; GELU against
 the float64 formula; the residual-stream gradient at the backward tolerance;
-column sums (db1, db2, dgamma, dbeta) at the column-sum tolerance."""
+column sums (db1, db2, dgamma, dbeta) at the column-sum tolerance.  The
+"fp16" case is the reference's fp16-storage path (half copy of the FFN
+activation, half-mask ReLU backward), with the half bits checked exactly."""
 import os
 import subprocess
 
@@ -31,7 +33,7 @@ def _load(d, name, shape, dtype=np.float32):
     return np.fromfile(os.path.join(d, name + ".bin"), dtype=dtype).reshape(shape)
 
 
-@pytest.mark.parametrize("act", ["relu", "gelu"])
+@pytest.mark.parametrize("act", ["relu", "gelu", "fp16"])
 def test_transformer_nongemm_sequence_and_graph_replay(dev, tmp_path, act):
     if not os.path.exists(EXE):
         pytest.fail(f"{EXE} is not built: run __graft_entry__.build() first")
@@ -68,6 +70,14 @@ def test_transformer_nongemm_sequence_and_graph_replay(dev, tmp_path, act):
     if act == "relu":
         act_ref = O.bias_relu_forward(s_ffh, b1)
         assert_exact("ff_act (bias+ReLU)", ld("ff_act", BT, FF), act_ref)
+    elif act == "fp16":
+        # CME213_FP16_STORAGE_ONLY: bias+ReLU in place, then the activation
+        # round-trips through its half copy (transformer.cu:315-321)
+        half_ref = O.float_to_half(O.bias_relu_forward(s_ffh, b1))
+        assert_exact("ff_relu_half", _load(d, "ff_relu_half", (-1,), np.uint16)[:BT * FF],
+                     half_ref.reshape(-1))
+        assert_exact("ff_hidden (ReLU through half)", ld("ff_hidden", BT, FF),
+                     O.half_to_float(half_ref))
     else:
         assert_fwd("ff_act (bias+GELU)", ld("ff_act", BT, FF), O.bias_gelu_forward_f64(s_ffh, b1))
     assert_exact("residual2", ld("residual2", BT, D), O.residual_add_with_bias(r1, s_ffo, b2))
@@ -84,6 +94,10 @@ def test_transformer_nongemm_sequence_and_graph_replay(dev, tmp_path, act):
     if act == "relu":
         gin, _ = O.relu_backward_with_bias_backward(act_ref, s_gact)
         assert_exact("grad_ff_hidden (ReLU)", ld("grad_ff_hidden", BT, FF), gin)
+        assert_colsum("db1", parts["db1"], gin.astype(np.float64).sum(0), gin)
+    elif act == "fp16":
+        gin, _ = O.relu_backward_with_bias_backward_half_mask(half_ref, s_gact)
+        assert_exact("grad_ff_hidden (half mask)", ld("grad_ff_hidden", BT, FF), gin)
         assert_colsum("db1", parts["db1"], gin.astype(np.float64).sum(0), gin)
     else:
         gin64, db64 = O.gelu_backward_with_bias_backward_f64(s_ffh, b1, s_gact)
