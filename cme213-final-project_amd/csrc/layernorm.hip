@@ -317,10 +317,12 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void ln_bwd_group_kernel(
     // every wave.  RF rows are loaded before the first is processed; rows
     // are still processed, and summed into ag/ab, in increasing order.  With
     // one wave per row (G = 1) one row in flight measured fastest ([8192,
-    // 768]: 2 or 4 rows were 0.4-0.5 us slower); with several waves per row
-    // two rows in flight were faster ([8192, 1600]: 34.0 against 36.7 us;
-    // [32768, 1600]: 109.5 against 123.6 us).
-    constexpr int RF = G > 1 ? 2 : 1;
+    // 768]: 2 or 4 rows were 0.4-0.5 us slower).  With several waves per row
+    // and at most 2 vectors per lane, two rows in flight were faster ([8192,
+    // 1600]: 34.0 against 36.7 us; [32768, 1600]: 109.0 against 124.1 us);
+    // with 4 vectors per lane the second row costs occupancy ([32768, 4096]:
+    // 290 against 269 us).
+    constexpr int RF = (G > 1 && N <= 2) ? 2 : 1;
     const int first = blockIdx.x * GPB;
     const int iters = first < rows ? (rows - first + stride - 1) / stride : 0;
     // Row numbers are 64-bit: with rows near INT_MAX, row + r * stride may
@@ -431,15 +433,18 @@ int pick_n(int need) {
     return 0;
 }
 
-// Rows per wave of the forward kernel, from a sweep over rows x {768, 1600}
-// on MI355X.  Two rows per wave measured faster for 6M-16M elements when
-// there are at least 6144 rows ([8192, 768]: 9.2 against 9.6 us; [6144,
-// 1600]: 14.6 against 16.5 us; [8192, 1600]: 18.4 against 21.2 us), one row
-// per wave elsewhere ([4096, 768]: 5.5 against 6.8 us; [4096, 1600]: 9.8
-// against 10.6 us; [12288, 1600]: 29.5 against 32.0 us; [65536, 768]: 67.4
-// against 70.5 us).
+// Rows per wave of the forward kernel, from a sweep over rows x {768, 1600,
+// 4096} on MI355X.  Two rows per wave measured faster for 6M-16M elements
+// when there are at least 6144 rows ([8192, 768]: 9.2 against 9.6 us;
+// [6144, 1600]: 14.6 against 16.5 us; [8192, 1600]: 18.4 against 21.2 us),
+// and for 4096-wide rows from 8192 rows ([8192, 4096]: 48.1 against 50.4
+// us; [32768, 4096]: 184.3 against 189.4 us); one row per wave elsewhere
+// ([4096, 768]: 5.5 against 6.8 us; [4096, 1600]: 9.8 against 10.6 us;
+// [12288, 1600]: 29.5 against 32.0 us; [65536, 768]: 67.4 against 70.5 us;
+// [2048, 4096]: 12.9 against 14.5 us).
 int fwd_rows_per_wave(int rows, int cols) {
     const long long elems = static_cast<long long>(rows) * cols;
+    if (cols >= 4096) return rows >= 8192 ? 2 : 1;
     return (rows >= 6144 && elems >= (6ll << 20) && elems <= (16ll << 20)) ? 2 : 1;
 }
 
