@@ -115,6 +115,35 @@ def test_heavy_hitter_and_invalid_ids(dev):
     assert_exact("valid rows", o[valid], wte[ids[valid]])
 
 
+def test_single_id_across_passes_and_windows(dev):
+    # 40000 tokens of one id: one owning workgroup sees 3 passes over the ids
+    # and 2048-entry windows in each, so the row is carried from window to
+    # window and pass to pass by different waves (ordered by the barriers)
+    V, D, BT = 7, 64, 40000
+    r = np.random.default_rng(77)
+    ids = np.full(BT, 5, np.int32)
+    ids[::997] = 2                  # a second, sparse id in the same windows
+    g = r.standard_normal((BT, D), dtype=np.float32)
+    dwte0 = r.standard_normal((V, D), dtype=np.float32)
+    Dwte = dev_t(dwte0)
+    M.embedding_backward(dev_t(g), dev_t(ids), Dwte, BT, D, V)
+    assert_exact("dwte single id", host(Dwte), O.embedding_backward(g, ids, dwte0))
+
+
+def test_trusted_ids_skip_negative(dev):
+    # vocab <= 0 trusts the ids; negative ids are still skipped
+    V, D, BT = 50, 32, 3000
+    r = np.random.default_rng(78)
+    ids = r.integers(0, V, BT).astype(np.int32)
+    ids[::7] = -1
+    g = r.standard_normal((BT, D), dtype=np.float32)
+    Dwte = torch.zeros(V, D, device=dev)
+    M.embedding_backward(dev_t(g), dev_t(ids), Dwte, BT, D, 0)
+    ok = ids >= 0
+    assert_exact("dwte trusted ids", host(Dwte),
+                 O.embedding_backward(g[ok], ids[ok], np.zeros((V, D), np.float32)))
+
+
 def test_embedding_backward_deterministic(dev):
     V, D, B, T = 50257, 768, 16, 1024
     _, _, ids, g = emb_inputs(V, D, B, T, 31)
