@@ -102,7 +102,7 @@ def test_transformer_nongemm_sequence_and_graph_replay(dev, tmp_path, act):
     else:
         gin64, db64 = O.gelu_backward_with_bias_backward_f64(s_ffh, b1, s_gact)
         assert_bwd("grad_ff_hidden (GELU)", ld("grad_ff_hidden", BT, FF), gin64)
-        assert_colsum("db1", parts["db1"], db64, gin64)
+        assert_colsum("db1", parts["db1"], db64, gin64, approx_terms=True)
     gres, dg2, db2ln = O.layernorm_backward(s_gl2, r1, m2, s2, ln2g, grad_x=s_gr2.copy(),
                                             add_to_grad=True)
     gres, dg1, db1ln = O.layernorm_backward(s_gl1, emb, m1, s1, ln1g, grad_x=gres,

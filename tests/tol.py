@@ -9,7 +9,9 @@ Element-wise backward outputs (dx, grad_in):     |gpu - ref| <= 1e-5 s + 1e-4 |r
 Column sums (dgamma, dbeta, dbias):              |gpu - ref| <= 1e-4 (|ref| + ||t_c||_2)
     where t_c are the per-row terms summed into column c; the float error of
     any summation order scales with ||t_c||_2, so a column whose sum cancels
-    to near zero is still held to 1e-4 of its natural size.
+    to near zero is still held to 1e-4 of its natural size.  Where the terms
+    are approximations of a function (GELU dbias against float64), the
+    element-wise backward floor 1e-5 s is added, times sqrt(rows).
 Gather / copies / single adds / selects:         bit-exact.
 
 Where a float oracle is itself inexact in a region (the textbook float GELU
@@ -49,12 +51,23 @@ def assert_bwd(name, gpu, ref):
     return _report(name, np.asarray(gpu), ref, bound)
 
 
-def assert_colsum(name, gpu, ref, terms):
-    """terms: [rows, cols] array of the per-row summands (float64 ok)."""
+def assert_colsum(name, gpu, ref, terms, approx_terms=False):
+    """terms: [rows, cols] array of the per-row summands (float64 ok).
+
+    approx_terms: the summands are themselves fp32 approximations of a
+    function (the GELU gradient against its float64 value), each held to the
+    element-wise backward tolerance; their absolute floor BWD_ATOL * s, with
+    s = max(1, rms(terms)), then also bounds the column sum, accumulated as
+    independent errors (times sqrt(rows)).  Without it a column of one row
+    would be held to 1e-4 of a gradient value whose own element bound is
+    BWD_ATOL * s."""
     ref = np.asarray(ref)
     t = np.asarray(terms, dtype=np.float64)
     l2 = np.sqrt((t * t).sum(axis=0))
     bound = COL_RTOL * (np.abs(ref.astype(np.float64)) + l2)
+    if approx_terms and t.size:
+        s = max(1.0, float(np.sqrt(np.mean(t * t))))
+        bound = bound + BWD_ATOL * s * np.sqrt(t.shape[0])
     return _report(name, np.asarray(gpu), ref, bound)
 
 
