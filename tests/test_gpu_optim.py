@@ -118,3 +118,24 @@ def test_gpt2_small_parameter_count(dev):
                                 bc2, 1.0)
     assert_exact("param", host(P_), po)
     assert_exact("m", host(Mm), mo)
+
+
+def test_adam_past_one_vector_per_thread(dev):
+    # 2^25 + 1 vectors: one more than the one-vector-per-thread grid covers,
+    # so the last vector goes through the kernel's grid-stride loop
+    n = (1 << 27) + 4
+    note(f"adam_clipped n={n}")
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(9)
+    P_ = torch.randn(n, device="cuda", generator=gen)
+    G_ = torch.randn(n, device="cuda", generator=gen)
+    Mm = torch.randn(n, device="cuda", generator=gen) * 0.1
+    V_ = torch.rand(n, device="cuda", generator=gen) * 0.01
+    p, g, m, v = host(P_), host(G_), host(Mm), host(V_)
+    clip = torch.full((1,), 0.75, device="cuda")
+    bc1, bc2 = O.adam_bias_corrections(0.9, 0.999, 4)
+    M.adam_clipped(P_, G_, Mm, V_, clip, 3e-4, 0.9, 0.999, 1e-8, bc1, bc2, 1.0, n)
+    po, mo, vo = O.adam_clipped(p, g, m, v, 0.75, 3e-4, 0.9, 0.999, 1e-8, bc1, bc2, 1.0)
+    assert_exact("param", host(P_), po)
+    assert_exact("m", host(Mm), mo)
+    assert_exact("v", host(V_), vo)
