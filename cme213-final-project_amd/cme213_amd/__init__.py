@@ -98,6 +98,7 @@ _SIGS = {
     "mi_pos_embedding_forward": (c_int, [P, P, c_int, c_int, c_int, P]),
     "mi_pos_embedding_backward": (c_int, [P, P, c_int, c_int, c_int, P]),
     "mi_embedding_pos_forward": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, P]),
+    "mi_embedding_pos_backward": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, P]),
     # softmax / cross-entropy
     "mi_softmax_forward": (c_int, [P, P, c_int, c_int, P]),
     "mi_cross_entropy_forward": (c_int, [P, P, P, c_int, c_int, P, P]),
@@ -299,6 +300,15 @@ def pos_embedding_backward(grad_out, grad_pos_table, batch, seq, dim, stream=Non
 def embedding_pos_forward(table, pos_table, tokens, out, batch, seq, dim, vocab=0, stream=None):
     _check(lib.mi_embedding_pos_forward(_f(table), _f(pos_table), _i(tokens), _f(out), batch,
                                         seq, dim, vocab, _stream(stream)))
+
+
+def embedding_pos_backward(grad_out, tokens, grad_table, grad_pos_table, batch, seq, dim, vocab=0,
+                           stream=None):
+    """embedding_backward + pos_embedding_backward in one launch (bit-identical to the two
+    calls); the reference calls them back to back at FC/src/model/transformer.cu:581-584."""
+    _check(lib.mi_embedding_pos_backward(_f(grad_out), _i(tokens), _f(grad_table),
+                                         _f(grad_pos_table), batch, seq, dim, vocab,
+                                         _stream(stream)))
 
 
 def softmax_forward(x, out, rows, cols, stream=None):

@@ -13,7 +13,7 @@ from __future__ import annotations
 import torch
 
 from . import (adam_update, bias_gelu_forward, bias_relu_forward_to_half,
-               cross_entropy_forward_v2, embedding_backward, embedding_pos_forward,
+               cross_entropy_forward_v2, embedding_pos_backward, embedding_pos_forward,
                gelu_backward_with_bias_backward, layernorm_backward, layernorm_backward_residual,
                layernorm_forward_save, pos_embedding_backward,
                relu_backward_with_bias_backward_half_mask, residual_layernorm_forward_save)
@@ -260,8 +260,8 @@ class Embedding:
         return [
             ("emb_fwd", lambda: embedding_pos_forward(self.wte, self.wpe, s["ids"], s["out"], B, T,
                                                       D, V)),
-            ("emb_bwd", lambda: (embedding_backward(s["dout"], s["ids"], self.dwte, B * T, D, V),
-                                 pos_embedding_backward(s["dout"], self.dwpe, B, T, D))),
+            ("emb_bwd", lambda: embedding_pos_backward(s["dout"], s["ids"], self.dwte, self.dwpe,
+                                                       B, T, D, V)),
         ]
 
     def step(self, k):

@@ -15,7 +15,10 @@
 // whole id vector, sorts them by id in LDS and adds every id's rows in
 // position order; exactly one wave updates a given table row.
 // Position backward: one thread per (t, column vector) adds grad_out[b, t]
-// for b = 0, 1, ... in order onto grad_pos[t].
+// for b = 0, 1, ... in order onto grad_pos[t]; the fused token + position
+// backward does the same sums inside the token kernel's workgroups.
+#include <type_traits>
+
 #include "mi_common.hpp"
 
 namespace mi {
@@ -134,11 +137,22 @@ constexpr int kOwnTake = 2;                      // sorted entries per claim
 constexpr int kOwnMaxK = 512;                    // owning workgroups, at most
 constexpr int kOwnTokens = 32;                   // tokens per owner, about
 
+// Position gradient fused into the owner kernel (POS): the workgroups also
+// share out the seq * nv position column vectors, one per thread per round;
+// each is grad_pos[t, j] + grad_out[0, t, j] + grad_out[1, t, j] + ... in
+// increasing b, the order of pos_bwd_kernel.  The old values and the first
+// kPosPre batch rows of a thread's first vector are requested before the
+// id scan and summed after it, so that they stream from HBM while the
+// workgroup scans ids and builds its list (HBM is otherwise idle then).
+constexpr int kPosPre = 7;   // batch rows in flight across the id scan, at most
+constexpr int kPosChunk = 5; // batch rows per group of loads afterwards
+
 // 128 VGPRs at most, so that two 8-wave workgroups fit on a CU.
-template <int W, int NCH>
+template <int W, int NCH, bool POS>
 __global__ __launch_bounds__(kOwnThreads) __attribute__((amdgpu_waves_per_eu(4))) void
 emb_bwd_owner_kernel(const int* __restrict__ ids, int n, int vocab, bool vec_ids,
-                     const float* __restrict__ g, float* __restrict__ table, int dim) {
+                     const float* __restrict__ g, float* __restrict__ table, int dim,
+                     float* __restrict__ gpos, int batch, int seq) {
     __shared__ __align__(16) int s_id[kOwnCap];  // list in position order
     __shared__ int s_pos[kOwnCap];
     __shared__ int s_sid[kOwnCap];  // list sorted by id
@@ -157,7 +171,7 @@ emb_bwd_owner_kernel(const int* __restrict__ ids, int n, int vocab, bool vec_ids
     // acc += the grad rows of sorted-list entries from, from + 1, ... while
     // they carry `id` (none if entry `from` does not), in list order, for
     // the column vectors c0 + lane + q * 64.
-    auto add_entries = [&](int id, int from, int L, int c0, fvec<W>(&acc)[NCH]) {
+    auto add_entries = [&](int id, int from, int L, int c0, fvec<W>(&acc)[NCH]) __attribute__((always_inline)) {
         for (int off = from;; off += kWave) {
             const int e = off + lane;
             const bool same = e < L && s_sid[e] == id;
@@ -192,7 +206,7 @@ emb_bwd_owner_kernel(const int* __restrict__ ids, int n, int vocab, bool vec_ids
 
     // Adds the run starting at sorted-list entry s0 (entries s0, s0 + 1, ...
     // with the id of s0, in position order) onto that id's table row.
-    auto add_run = [&](int s0, int L) {
+    auto add_run = [&](int s0, int L) __attribute__((always_inline)) {
         const int id = s_sid[s0];
         float* row = table + static_cast<size_t>(id) * dim;
         for (int c0 = 0; c0 < nv; c0 += NCH * kWave) {
@@ -214,7 +228,7 @@ emb_bwd_owner_kernel(const int* __restrict__ ids, int n, int vocab, bool vec_ids
     // Adds the runs starting at sorted-list entries sa and sb together: the
     // two table rows and the first grad row of each run are requested at
     // once; the rest of each run (if any) follows.
-    auto add_pair = [&](int sa, int sb, int L) {
+    auto add_pair = [&](int sa, int sb, int L) __attribute__((always_inline)) {
         const int ida = s_sid[sa];
         const int idb = s_sid[sb];
         float* ra = table + static_cast<size_t>(ida) * dim;
@@ -261,7 +275,7 @@ emb_bwd_owner_kernel(const int* __restrict__ ids, int n, int vocab, bool vec_ids
     // taker of an entry that starts a run of equal ids adds the whole run.
     // Each run is added by one wave, whichever it is, so the result does
     // not depend on the assignment.
-    auto process = [&](int L) {
+    auto process = [&](int L) __attribute__((always_inline)) {
         for (int i = static_cast<int>(threadIdx.x); i < L; i += kOwnThreads) {
             const int me = s_id[i];
             int r = 0;
@@ -298,7 +312,46 @@ emb_bwd_owner_kernel(const int* __restrict__ ids, int n, int vocab, bool vec_ids
         }
     };
 
-    for (long long base = 0; base < n; base += kOwnSpan) {
+    // Position gradient, first round: requests issued now, summed below.
+    const long long pvec = POS ? static_cast<long long>(seq) * nv : 0;   // position vectors
+    const long long pstride = static_cast<long long>(gridDim.x) * kOwnThreads;
+    const long long pv0 = static_cast<long long>(k) * kOwnThreads + threadIdx.x;
+    const size_t bstride = static_cast<size_t>(seq) * nv;                // vectors per batch row
+    // PRE batch rows of the first position vector are requested across the
+    // id scan (the most that stays within 128 VGPRs without spills: 7 for 2-3
+    // column vectors per lane, 4 for one); with 4 column vectors per lane
+    // none fit, and the position sums run after the token gradient instead.
+    constexpr int PRE = !POS ? 0 : NCH == 1 ? 4 : NCH <= 3 ? kPosPre : 0;
+    constexpr int NPQ = PRE > 0 ? PRE : 1;
+    // Adds batch rows b0, b0 + 1, ... of position vector pv onto acc, in
+    // order, and stores the total.
+    auto pos_rest = [&](long long pv, int b0, fvec<W> acc) __attribute__((always_inline)) {
+        for (int b = b0; b < batch; b += kPosChunk) {
+            fvec<W> q[kPosChunk];
+#pragma unroll
+            for (int u = 0; u < kPosChunk; ++u)
+                q[u] = b + u < batch ? sload<W>(g, (b + u) * bstride + pv) : vzero<W>();
+#pragma unroll
+            for (int u = 0; u < kPosChunk; ++u)
+                if (b + u < batch)
+#pragma unroll
+                    for (int x = 0; x < W; ++x) acc.v[x] = acc.v[x] + q[u].v[x];
+        }
+        vstore<W>(gpos, pv, acc);
+    };
+    // The position vectors after a thread's first one (pv0 + pstride, ...).
+    auto pos_others = [&]() __attribute__((always_inline)) {
+        for (long long pv = pv0 + pstride; pv < pvec; pv += pstride)
+            pos_rest(pv, 0, vload<W>(gpos, pv));
+    };
+
+    // One pass over kOwnSpan positions of the id vector.  The first pass is
+    // a separate instantiation (FIRST) so that the position registers live
+    // only inside it.  This lambda and those it calls are inlined: an
+    // out-of-line call keeps the captured locals in scratch memory.
+    auto pass = [&](long long base, auto first_tag) __attribute__((always_inline)) {
+        constexpr bool first = decltype(first_tag)::value && PRE > 0;
+        [[maybe_unused]] fvec<W> pacc, pq[NPQ];
         // Wave w reads positions base + w * kOwnPer * 64 + [0, kOwnPer * 64):
         // group j (4 ids per lane) covers 256 consecutive positions, lane l
         // takes positions 4l .. 4l + 3 of it, so every load instruction of
@@ -320,6 +373,19 @@ emb_bwd_owner_kernel(const int* __restrict__ ids, int n, int vocab, bool vec_ids
 #pragma unroll
                 for (int e = 0; e < 4; ++e) my[4 * j + e] = p4 + e < n ? ids[p4 + e] : -1;
             }
+        }
+        if constexpr (first) {
+            // Issued after the id loads: loads complete in issue order, so
+            // the scan can use its ids while these are still in flight.
+            if (pv0 < pvec) {
+                pacc = vload<W>(gpos, pv0);
+#pragma unroll
+                for (int u = 0; u < PRE; ++u)
+                    pq[u] = u < batch ? sload<W>(g, u * bstride + pv0) : vzero<W>();
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kOwnGroups; ++j) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int id = my[4 * j + e];
@@ -375,6 +441,17 @@ emb_bwd_owner_kernel(const int* __restrict__ ids, int n, int vocab, bool vec_ids
                 }
             }
         }
+        if constexpr (first) {
+            if (pv0 < pvec) {
+#pragma unroll
+                for (int u = 0; u < PRE; ++u)
+                    if (u < batch)
+#pragma unroll
+                        for (int x = 0; x < W; ++x) pacc.v[x] = pacc.v[x] + pq[u].v[x];
+                pos_rest(pv0, PRE, pacc);
+            }
+            pos_others();
+        }
         for (int w0 = 0; w0 < total; w0 += kOwnCap) {
             if (w0 > 0) {
 #pragma unroll 1
@@ -397,7 +474,49 @@ emb_bwd_owner_kernel(const int* __restrict__ ids, int n, int vocab, bool vec_ids
             process(total - w0 < kOwnCap ? total - w0 : kOwnCap);
             __syncthreads();
         }
+    };
+    if constexpr (PRE > 0) {
+        pass(0, std::true_type{});
+        for (long long base = kOwnSpan; base < n; base += kOwnSpan) pass(base, std::false_type{});
+    } else {
+        for (long long base = 0; base < n; base += kOwnSpan) pass(base, std::false_type{});
     }
+    if constexpr (POS && PRE == 0) {
+        if (pv0 < pvec) pos_rest(pv0, 0, vload<W>(gpos, pv0));
+        pos_others();
+    }
+}
+
+// One launch of the owner kernel: K = 2^log2k owning workgroups, about
+// kOwnTokens tokens each.  The position gradient (POS) needs 16-byte
+// alignment of grad_pos as well for the vector path.
+template <bool POS>
+void launch_owner(const float* grad_out, const int* tokens, float* grad_table, float* grad_pos,
+                  int batch_seq, int batch, int seq, int dim, int vocab, hipStream_t st) {
+    int log2k = 0;
+    while ((2 << log2k) <= kOwnMaxK && (2ll << log2k) * kOwnTokens <= batch_seq) ++log2k;
+    const dim3 grid(1u << log2k), block(kOwnThreads);
+    const bool vec_ids = aligned16(tokens);
+    const bool v4 = dim % 4 == 0 && aligned16(grad_out) && aligned16(grad_table) &&
+                    (!POS || aligned16(grad_pos));
+    const int nv = v4 ? dim / 4 : dim;
+    // Column vectors per lane held at once: just enough for the row, at most
+    // 4 (wider rows loop over column chunks).
+    const int nch = nv <= kWave ? 1 : nv <= 2 * kWave ? 2 : nv <= 3 * kWave ? 3 : 4;
+#define MI_OWNER_CASE(WW, NN)                                                                  \
+    hipLaunchKernelGGL((emb_bwd_owner_kernel<WW, NN, POS>), grid, block, 0, st, tokens,       \
+                       batch_seq, vocab, vec_ids, grad_out, grad_table, dim, grad_pos, batch, seq)
+    switch ((v4 ? 10 : 0) + nch) {
+        case 11: MI_OWNER_CASE(4, 1); break;
+        case 12: MI_OWNER_CASE(4, 2); break;
+        case 13: MI_OWNER_CASE(4, 3); break;
+        case 14: MI_OWNER_CASE(4, 4); break;
+        case 1: MI_OWNER_CASE(1, 1); break;
+        case 2: MI_OWNER_CASE(1, 2); break;
+        case 3: MI_OWNER_CASE(1, 3); break;
+        default: MI_OWNER_CASE(1, 4); break;
+    }
+#undef MI_OWNER_CASE
 }
 
 }  // namespace
@@ -497,31 +616,24 @@ int mi_embedding_backward(const float* grad_out, const int* tokens, float* grad_
         return set_error(MI_ERR_INVALID_ARG, "%s: batch_seq=%d dim=%d", name, batch_seq, dim);
     if (batch_seq == 0) return MI_OK;
     if (!grad_out || !tokens || !grad_table) return set_error(MI_ERR_INVALID_ARG, "%s: NULL", name);
-    hipStream_t st = to_stream(stream);
-    // K = 2^log2k owning workgroups, about kOwnTokens tokens each.
-    int log2k = 0;
-    while ((2 << log2k) <= kOwnMaxK && (2ll << log2k) * kOwnTokens <= batch_seq) ++log2k;
-    const dim3 grid(1u << log2k), block(kOwnThreads);
-    const bool vec_ids = aligned16(tokens);
-    const bool v4 = dim % 4 == 0 && aligned16(grad_out) && aligned16(grad_table);
-    const int nv = v4 ? dim / 4 : dim;
-    // Column vectors per lane held at once: just enough for the row, at most
-    // 4 (wider rows loop over column chunks).
-    const int nch = nv <= kWave ? 1 : nv <= 2 * kWave ? 2 : nv <= 3 * kWave ? 3 : 4;
-#define MI_OWNER_CASE(WW, NN)                                                                     \
-    hipLaunchKernelGGL((emb_bwd_owner_kernel<WW, NN>), grid, block, 0, st, tokens, batch_seq,    \
-                       vocab, vec_ids, grad_out, grad_table, dim)
-    switch ((v4 ? 10 : 0) + nch) {
-        case 11: MI_OWNER_CASE(4, 1); break;
-        case 12: MI_OWNER_CASE(4, 2); break;
-        case 13: MI_OWNER_CASE(4, 3); break;
-        case 14: MI_OWNER_CASE(4, 4); break;
-        case 1: MI_OWNER_CASE(1, 1); break;
-        case 2: MI_OWNER_CASE(1, 2); break;
-        case 3: MI_OWNER_CASE(1, 3); break;
-        default: MI_OWNER_CASE(1, 4); break;
-    }
-#undef MI_OWNER_CASE
+    launch_owner<false>(grad_out, tokens, grad_table, nullptr, batch_seq, 0, 1, dim, vocab,
+                        to_stream(stream));
+    return check_launch(name);
+}
+
+int mi_embedding_pos_backward(const float* grad_out, const int* tokens, float* grad_table,
+                              float* grad_pos_table, int batch, int seq, int dim, int vocab,
+                              void* stream) {
+    const char* name = "mi_embedding_pos_backward";
+    if (batch < 0 || seq <= 0 || dim <= 0)
+        return set_error(MI_ERR_INVALID_ARG, "%s: batch=%d seq=%d dim=%d", name, batch, seq, dim);
+    const long long bt = static_cast<long long>(batch) * seq;
+    if (bt == 0) return MI_OK;
+    if (bt > INT32_MAX) return set_error(MI_ERR_INVALID_ARG, "%s: batch*seq too large", name);
+    if (!grad_out || !tokens || !grad_table || !grad_pos_table)
+        return set_error(MI_ERR_INVALID_ARG, "%s: NULL", name);
+    launch_owner<true>(grad_out, tokens, grad_table, grad_pos_table, static_cast<int>(bt), batch,
+                       seq, dim, vocab, to_stream(stream));
     return check_launch(name);
 }
 

@@ -186,6 +186,15 @@ int mi_embedding_pos_forward(const float* table, const float* pos_table,
                              const int* tokens, float* out,
                              int batch, int seq, int dim, int vocab, void* stream);
 
+/* Fused token + position backward: mi_embedding_backward(grad_out, tokens,
+ * grad_table, batch * seq, dim, vocab) and mi_pos_embedding_backward(grad_out,
+ * grad_pos_table, batch, seq, dim) in one launch, bit-identical to the two
+ * calls (same accumulation orders).  The reference issues the two calls back
+ * to back (FINAL_CLEAN_CODE/src/model/transformer.cu:581-584). */
+int mi_embedding_pos_backward(const float* grad_out, const int* tokens,
+                              float* grad_table, float* grad_pos_table,
+                              int batch, int seq, int dim, int vocab, void* stream);
+
 /* ----- softmax and cross-entropy ----------------------------------------- */
 
 /* out[r, :] = exp(x[r, :] - max) / sum, per row.  Replaces softmax_forward

@@ -49,6 +49,11 @@ def test_host_side_argument_errors():
     assert lib.mi_bias_gelu_forward(None, None, None, -2, 8, None) == M.MI_ERR_INVALID_ARG
     assert lib.mi_residual_add(None, None, None, -5, None) == M.MI_ERR_INVALID_ARG
     assert lib.mi_embedding_backward(None, None, None, 16, 0, 0, None) == M.MI_ERR_INVALID_ARG
+    assert lib.mi_embedding_pos_backward(None, None, None, None, 4, 0, 64, 0,
+                                         None) == M.MI_ERR_INVALID_ARG
+    assert lib.mi_embedding_pos_backward(None, None, None, None, 4, 8, 64, 0,
+                                         None) == M.MI_ERR_INVALID_ARG
+    assert "NULL" in M.last_error()
     # NULL pointers with a non-empty shape are rejected
     assert lib.mi_layernorm_forward_save(None, None, None, None, None, None, 4, 8, 1e-5,
                                          None) == M.MI_ERR_INVALID_ARG
@@ -68,6 +73,7 @@ def test_host_side_argument_errors():
     assert lib.mi_layernorm_forward(None, None, None, None, 0, 768, 1e-5, None) == M.MI_OK
     assert lib.mi_residual_add(None, None, None, 0, None) == M.MI_OK
     assert lib.mi_embedding_forward(None, None, None, 0, 768, 0, None) == M.MI_OK
+    assert lib.mi_embedding_pos_backward(None, None, None, None, 0, 8, 64, 0, None) == M.MI_OK
     assert lib.mi_softmax_forward(None, None, 0, 10, None) == M.MI_OK
 
 

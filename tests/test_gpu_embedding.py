@@ -91,6 +91,12 @@ def test_embedding_forward_backward(dev, V, D, B, T, vocab_arg):
     assert_exact("dwte", host(Dwte), O.embedding_backward(g, ids, dwte0))
     assert_exact("dwpe", host(Dwpe), O.pos_embedding_backward(g, dwpe0, B, T))
 
+    # fused token + position backward: bit-identical to the two calls
+    Fwte, Fwpe = dev_t(dwte0), dev_t(dwpe0)
+    M.embedding_pos_backward(G, Ids, Fwte, Fwpe, B, T, D, vocab_arg)
+    assert_exact("fused dwte", host(Fwte), host(Dwte))
+    assert_exact("fused dwpe", host(Fwpe), host(Dwpe))
+
 
 def test_heavy_hitter_and_invalid_ids(dev):
     V, D, B, T = 300, 64, 4, 1100
@@ -107,6 +113,11 @@ def test_heavy_hitter_and_invalid_ids(dev):
     M.embedding_backward(G, Ids, Dwte, BT, D, V)
     expect = O.embedding_backward(g[valid], ids[valid], np.zeros((V, D), np.float32))
     assert_exact("dwte heavy hitter", host(Dwte), expect)
+    Fwte, Fwpe = torch.zeros(V, D, device=dev), torch.zeros(T, D, device=dev)
+    M.embedding_pos_backward(G, Ids, Fwte, Fwpe, B, T, D, V)
+    assert_exact("fused dwte heavy hitter", host(Fwte), expect)
+    assert_exact("fused dwpe, every row counted", host(Fwpe),
+                 O.pos_embedding_backward(g, np.zeros((T, D), np.float32), B, T))
 
     out = torch.empty(BT, D, device=dev)
     M.embedding_forward(dev_t(wte), Ids, out, BT, D, V)
@@ -128,6 +139,14 @@ def test_single_id_across_passes_and_windows(dev):
     Dwte = dev_t(dwte0)
     M.embedding_backward(dev_t(g), dev_t(ids), Dwte, BT, D, V)
     assert_exact("dwte single id", host(Dwte), O.embedding_backward(g, ids, dwte0))
+    # fused with the position gradient, B = 8 rows of T = 5000 positions: the
+    # first pass requests position loads across its scan, two more passes follow
+    B, T = 8, BT // 8
+    dwpe0 = r.standard_normal((T, D), dtype=np.float32)
+    Fwte, Fwpe = dev_t(dwte0), dev_t(dwpe0)
+    M.embedding_pos_backward(dev_t(g), dev_t(ids), Fwte, Fwpe, B, T, D, V)
+    assert_exact("fused dwte single id", host(Fwte), host(Dwte))
+    assert_exact("fused dwpe", host(Fwpe), O.pos_embedding_backward(g, dwpe0, B, T))
 
 
 def test_trusted_ids_skip_negative(dev):
