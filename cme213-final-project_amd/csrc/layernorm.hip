@@ -342,17 +342,29 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void ln_bwd_group_kernel(
     // Row numbers are 64-bit: with rows near INT_MAX, row + r * stride may
     // exceed the int range for the masked tail.
     long long row = first + grp;
-    for (int i = 0; i < iters; i += RF, row += static_cast<long long>(RF) * stride) {
+    // At least one trip: every launched workgroup has a row (the grid is at
+    // most ceil(rows / GPB) workgroups), and a trip over masked rows only
+    // adds zeros.  With a possible zero-trip path the compiler kept gamma's
+    // loads outstanding past the loop and waited for every store (vmcnt(0))
+    // before the combine below.
+    int i = 0;
+    do {
         RowIn cur[RF];
 #pragma unroll
         for (int r = 0; r < RF; ++r) load_row(row + r * stride, cur[r]);
 #pragma unroll
         for (int r = 0; r < RF; ++r) process(cur[r], row + r * stride, (i + r) & 1);
-    }
+        i += RF;
+        row += static_cast<long long>(RF) * stride;
+    } while (i < iters);
 
     // Combine the GPB groups' running sums in a fixed binary-tree order
     // (level h adds group g + h into group g, for h = GPB/2 ... 1).
-    if (ln_bwd_flat_combine(GPB, cols)) {
+    // Every width this instantiation handles (at most N*W*GT columns) may
+    // fit the staging; then the choice needs no run-time test.
+    constexpr bool kFlatAll = GPB >= 4 && static_cast<size_t>(GPB) * 2 * N * W * GT *
+                                              sizeof(float) <= kFlatCombineLds;
+    if (kFlatAll || ln_bwd_flat_combine(GPB, cols)) {
         // One barrier: every group stages its sums as a [2*cols] row
         // (dgamma then dbeta) in LDS, then each thread finishes a few
         // columns of the partial row, adding the GPB staged values in the
