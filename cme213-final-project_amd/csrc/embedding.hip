@@ -30,32 +30,61 @@ constexpr int kRowWaves = 4;   // token rows per workgroup
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
-template <int W, bool POS>
+// Each wave gathers R consecutive token rows: the R ids are read first,
+// then the loads of all R rows (table and position, NQ vectors per lane per
+// row at a time) are issued before any row is stored, so that R row gathers
+// are in flight per wave instead of one behind each id load.
+template <int W, bool POS, int R, int NQ>
 __global__ __launch_bounds__(kRowWaves * kWave) void emb_fwd_kernel(
     const float* __restrict__ table, const float* __restrict__ pos, const int* __restrict__ tokens,
     float* __restrict__ out, int batch_seq, int seq, int dim, int vocab) {
     const int lane = threadIdx.x & (kWave - 1);
-    const int i = blockIdx.x * kRowWaves + static_cast<int>(threadIdx.x / kWave);
-    if (i >= batch_seq) return;
-    const int id = tokens[i];
-    const bool ok = vocab <= 0 || (id >= 0 && id < vocab);
+    const int i0 = (blockIdx.x * kRowWaves + static_cast<int>(threadIdx.x / kWave)) * R;
+    if (i0 >= batch_seq) return;  // wave-uniform
     const int nv = dim / W;
-    const float* src = table + static_cast<size_t>(ok ? id : 0) * dim;
-    const float* p = POS ? pos + static_cast<size_t>(i % seq) * dim : nullptr;
-    float* dst = out + static_cast<size_t>(i) * dim;
-#pragma unroll 4
-    for (int j = lane; j < nv; j += kWave) {
-        // Table rows are gathered with the non-temporal hint: in the config-2
-        // step (forward after the previous backward) it measured 65.1 -> 64.1
-        // us, although a forward repeated alone, which finds the 154 MB
-        // table in the last-level cache, is faster without it (15.9 us).
-        fvec<W> v = ok ? sload<W>(src, j) : vzero<W>();
-        if constexpr (POS) {
-            const fvec<W> q = vload<W>(p, j);
+    int id[R];
+    bool ok[R];
 #pragma unroll
-            for (int e = 0; e < W; ++e) v.v[e] = v.v[e] + q.v[e];
+    for (int r = 0; r < R; ++r) {
+        const int i = i0 + r < batch_seq ? i0 + r : batch_seq - 1;
+        id[r] = tokens[i];
+        ok[r] = i0 + r < batch_seq && (vocab <= 0 || (id[r] >= 0 && id[r] < vocab));
+    }
+    for (int j0 = lane; j0 < nv; j0 += NQ * kWave) {
+        fvec<W> v[R][NQ];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float* src = table + static_cast<size_t>(ok[r] ? id[r] : 0) * dim;
+            const float* p = POS ? pos + static_cast<size_t>((i0 + r) % seq) * dim : nullptr;
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                const int j = j0 + q * kWave;
+                // Table rows are gathered with the non-temporal hint: in the
+                // config-2 step (forward after the previous backward) it
+                // measured 65.1 -> 64.1 us, although a forward repeated
+                // alone, which finds the 154 MB table in the last-level
+                // cache, is faster without it (15.9 us).
+                v[r][q] = (ok[r] && j < nv) ? sload<W>(src, j) : vzero<W>();
+                if constexpr (POS) {
+                    if (j < nv && i0 + r < batch_seq) {
+                        const fvec<W> t = vload<W>(p, j);
+#pragma unroll
+                        for (int e = 0; e < W; ++e) v[r][q].v[e] = v[r][q].v[e] + t.v[e];
+                    }
+                }
+            }
         }
-        sstore<W>(dst, j, v);  // streamed out: measured 20.9 -> 16.0 us at config 2
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (i0 + r >= batch_seq) break;  // wave-uniform
+            float* dst = out + static_cast<size_t>(i0 + r) * dim;
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                const int j = j0 + q * kWave;
+                // streamed out: measured 20.9 -> 16.0 us at config 2
+                if (j < nv) sstore<W>(dst, j, v[r][q]);
+            }
+        }
     }
 }
 
@@ -487,6 +516,40 @@ emb_bwd_owner_kernel(const int* __restrict__ ids, int n, int vocab, bool vec_ids
     }
 }
 
+#ifndef MI_EMB_ROWS
+#define MI_EMB_ROWS 4
+#endif
+// Token rows per wave in the forward gather.  Config 2 step (V = 50257,
+// D = 768, 16384 tokens): 1 row 60.1 us, 2 rows 60.7, 4 rows 59.1, 8 rows 63.8.
+constexpr int kEmbRows = MI_EMB_ROWS;
+
+// Forward gather launch: kEmbRows rows per wave, NQ = vectors per lane per
+// row at a time (just enough for the row, at most 4).
+template <bool POS>
+void launch_emb_fwd(const float* table, const float* pos, const int* tokens, float* out,
+                    int batch_seq, int seq, int dim, int vocab, hipStream_t st) {
+    const bool v4 = dim % 4 == 0 && aligned16(table) && aligned16(out) && (!POS || aligned16(pos));
+    const int nv = v4 ? dim / 4 : dim;
+    const int nq = nv <= kWave ? 1 : nv <= 2 * kWave ? 2 : nv <= 3 * kWave ? 3 : 4;
+    const long long waves = (static_cast<long long>(batch_seq) + kEmbRows - 1) / kEmbRows;
+    const dim3 grid(static_cast<unsigned>((waves + kRowWaves - 1) / kRowWaves)),
+        block(kRowWaves * kWave);
+#define MI_FWD_CASE(WW, QQ)                                                                     \
+    hipLaunchKernelGGL((emb_fwd_kernel<WW, POS, kEmbRows, QQ>), grid, block, 0, st, table, pos, \
+                       tokens, out, batch_seq, seq, dim, vocab)
+    switch ((v4 ? 10 : 0) + nq) {
+        case 11: MI_FWD_CASE(4, 1); break;
+        case 12: MI_FWD_CASE(4, 2); break;
+        case 13: MI_FWD_CASE(4, 3); break;
+        case 14: MI_FWD_CASE(4, 4); break;
+        case 1: MI_FWD_CASE(1, 1); break;
+        case 2: MI_FWD_CASE(1, 2); break;
+        case 3: MI_FWD_CASE(1, 3); break;
+        default: MI_FWD_CASE(1, 4); break;
+    }
+#undef MI_FWD_CASE
+}
+
 // One launch of the owner kernel: K = 2^log2k owning workgroups, about
 // kOwnTokens tokens each.  The position gradient (POS) needs 16-byte
 // alignment of grad_pos as well for the vector path.
@@ -535,14 +598,8 @@ int mi_embedding_forward(const float* table, const int* tokens, float* out, int 
         return set_error(MI_ERR_INVALID_ARG, "%s: batch_seq=%d dim=%d", name, batch_seq, dim);
     if (batch_seq == 0) return MI_OK;
     if (!table || !tokens || !out) return set_error(MI_ERR_INVALID_ARG, "%s: NULL", name);
-    const dim3 grid((batch_seq + kRowWaves - 1) / kRowWaves), block(kRowWaves * kWave);
-    hipStream_t st = to_stream(stream);
-    if (dim % 4 == 0 && aligned16(table) && aligned16(out))
-        hipLaunchKernelGGL((emb_fwd_kernel<4, false>), grid, block, 0, st, table, nullptr, tokens,
-                           out, batch_seq, 1, dim, vocab);
-    else
-        hipLaunchKernelGGL((emb_fwd_kernel<1, false>), grid, block, 0, st, table, nullptr, tokens,
-                           out, batch_seq, 1, dim, vocab);
+    launch_emb_fwd<false>(table, nullptr, tokens, out, batch_seq, 1, dim, vocab,
+                          to_stream(stream));
     return check_launch(name);
 }
 
@@ -556,15 +613,8 @@ int mi_embedding_pos_forward(const float* table, const float* pos_table, const i
     if (bt > INT32_MAX) return set_error(MI_ERR_INVALID_ARG, "%s: batch*seq too large", name);
     if (!table || !pos_table || !tokens || !out)
         return set_error(MI_ERR_INVALID_ARG, "%s: NULL", name);
-    const dim3 grid(static_cast<unsigned>((bt + kRowWaves - 1) / kRowWaves)),
-        block(kRowWaves * kWave);
-    hipStream_t st = to_stream(stream);
-    if (dim % 4 == 0 && aligned16(table) && aligned16(pos_table) && aligned16(out))
-        hipLaunchKernelGGL((emb_fwd_kernel<4, true>), grid, block, 0, st, table, pos_table, tokens,
-                           out, static_cast<int>(bt), seq, dim, vocab);
-    else
-        hipLaunchKernelGGL((emb_fwd_kernel<1, true>), grid, block, 0, st, table, pos_table, tokens,
-                           out, static_cast<int>(bt), seq, dim, vocab);
+    launch_emb_fwd<true>(table, pos_table, tokens, out, static_cast<int>(bt), seq, dim, vocab,
+                         to_stream(stream));
     return check_launch(name);
 }
 
