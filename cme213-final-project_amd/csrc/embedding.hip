@@ -172,7 +172,9 @@ constexpr int kOwnTokens = 32;                   // tokens per owner, about
 // increasing b, the order of pos_bwd_kernel.  The old values and the first
 // kPosPre batch rows of a thread's first vector are requested before the
 // id scan and summed after it, so that they stream from HBM while the
-// workgroup scans ids and builds its list (HBM is otherwise idle then).
+// workgroup scans ids and builds its list (HBM is otherwise idle then); the
+// partial sums wait in LDS, and the remaining rows are added after the
+// token gradient.
 constexpr int kPosPre = 7;   // batch rows in flight across the id scan, at most
 constexpr int kPosChunk = 5; // batch rows per group of loads afterwards
 
@@ -188,6 +190,7 @@ emb_bwd_owner_kernel(const int* __restrict__ ids, int n, int vocab, bool vec_ids
     __shared__ int s_spos[kOwnCap];
     __shared__ int s_wsum[kOwnWaves];
     __shared__ int s_next;
+    __shared__ fvec<W> s_pacc[POS ? kOwnThreads : 1];  // first position rows, summed
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = static_cast<int>(threadIdx.x / kWave);
     // gridDim.x is a power of two, so id % gridDim.x is a mask.
@@ -347,9 +350,11 @@ emb_bwd_owner_kernel(const int* __restrict__ ids, int n, int vocab, bool vec_ids
     const long long pv0 = static_cast<long long>(k) * kOwnThreads + threadIdx.x;
     const size_t bstride = static_cast<size_t>(seq) * nv;                // vectors per batch row
     // PRE batch rows of the first position vector are requested across the
-    // id scan (the most that stays within 128 VGPRs without spills: 7 for 2-3
-    // column vectors per lane, 4 for one); with 4 column vectors per lane
-    // none fit, and the position sums run after the token gradient instead.
+    // id scan (7 for 2-3 column vectors per lane, 4 for one: more spills
+    // registers in the scan); with 4 column vectors per lane none fit, and the
+    // position sums run after the token gradient alone.  The position
+    // bookkeeping kept across the token updates costs 2 spilled registers at
+    // 3 column vectors per lane, touched once before and once after them.
     constexpr int PRE = !POS ? 0 : NCH == 1 ? 4 : NCH <= 3 ? kPosPre : 0;
     constexpr int NPQ = PRE > 0 ? PRE : 1;
     // Adds batch rows b0, b0 + 1, ... of position vector pv onto acc, in
@@ -477,9 +482,8 @@ emb_bwd_owner_kernel(const int* __restrict__ ids, int n, int vocab, bool vec_ids
                     if (u < batch)
 #pragma unroll
                         for (int x = 0; x < W; ++x) pacc.v[x] = pacc.v[x] + pq[u].v[x];
-                pos_rest(pv0, PRE, pacc);
+                s_pacc[threadIdx.x] = pacc;  // finished after the token gradient
             }
-            pos_others();
         }
         for (int w0 = 0; w0 < total; w0 += kOwnCap) {
             if (w0 > 0) {
@@ -510,8 +514,16 @@ emb_bwd_owner_kernel(const int* __restrict__ ids, int n, int vocab, bool vec_ids
     } else {
         for (long long base = 0; base < n; base += kOwnSpan) pass(base, std::false_type{});
     }
-    if constexpr (POS && PRE == 0) {
-        if (pv0 < pvec) pos_rest(pv0, 0, vload<W>(gpos, pv0));
+    // The rest of the position sums follow the token gradient: the table-row
+    // updates start as soon as the list is built (config-2 step 58.8 ->
+    // 58.3 us against finishing the position sums first).
+    if constexpr (POS) {
+        if (pv0 < pvec) {
+            if constexpr (PRE > 0)
+                pos_rest(pv0, PRE, s_pacc[threadIdx.x]);
+            else
+                pos_rest(pv0, 0, vload<W>(gpos, pv0));
+        }
         pos_others();
     }
 }
