@@ -176,6 +176,16 @@ def test_embedding_backward_deterministic(dev):
             first = h
         else:
             assert_exact("repeat", h, first)
+    # the fused token + position backward: the same bits, call after call
+    pos_first = None
+    for _ in range(2):
+        Fwte, Fwpe = torch.zeros(V, D, device=dev), torch.zeros(T, D, device=dev)
+        M.embedding_pos_backward(G, Ids, Fwte, Fwpe, B, T, D, V)
+        assert_exact("fused repeat dwte", host(Fwte), first)
+        if pos_first is None:
+            pos_first = host(Fwpe)
+        else:
+            assert_exact("fused repeat dwpe", host(Fwpe), pos_first)
     # size-independent checks: total gradient mass is preserved per column
     # and untouched rows stay zero
     touched = np.zeros(V, bool)
