@@ -183,8 +183,9 @@ __global__ __launch_bounds__(kBlockThreads) void ln_fwd_block_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Backward, G waves per row, kBwdWaves waves per workgroup.
-// Dynamic LDS for the final combine of the GPB = kBwdWaves / G row groups:
+// Backward, G waves per row, NWV waves per workgroup (kBwdWaves, or 4 for
+// 4-wave rows of 4 vectors per lane, see plan_bwd).
+// Dynamic LDS for the final combine of the GPB = NWV / G row groups:
 // GPB rows of 2*cols floats for the one-barrier combine (used for GPB >= 4
 // when that fits in 64 KB), else (GPB/2) slots of 2*N*W*64*G floats for the
 // binary tree.  With GPB = 2 the tree is a single step and measured faster
@@ -200,15 +201,15 @@ __host__ __device__ inline bool ln_bwd_flat_combine(int gpb, int cols) {
                                sizeof(float) <= kFlatCombineLds;
 }
 
-template <int W, int N, int G, bool ADD>
-__global__ __launch_bounds__(kBwdWaves * kWave) void ln_bwd_group_kernel(
+template <int W, int N, int G, bool ADD, int NWV>
+__global__ __launch_bounds__(NWV * kWave) void ln_bwd_group_kernel(
     const float* __restrict__ gout, const float* __restrict__ x, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float* __restrict__ gamma, float* __restrict__ gx,
     float* __restrict__ part, int rows, int cols) {
-    constexpr int GPB = kBwdWaves / G;  // row groups per workgroup
+    constexpr int GPB = NWV / G;  // row groups per workgroup
     constexpr int GT = G * kWave;       // threads per group
     extern __shared__ float lds[];
-    __shared__ float red[2][kBwdWaves][2];
+    __shared__ float red[2][NWV][2];
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -383,7 +384,7 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void ln_bwd_group_kernel(
         __syncthreads();
         float* prow = part + static_cast<size_t>(blockIdx.x) * 2 * cols;
         const int tot = 2 * cols;
-        for (int c = threadIdx.x; c < tot; c += kBwdWaves * kWave) {
+        for (int c = threadIdx.x; c < tot; c += NWV * kWave) {
             float v[GPB];
 #pragma unroll
             for (int gi = 0; gi < GPB; ++gi) v[gi] = lds[static_cast<size_t>(gi) * tot + c];
@@ -571,6 +572,7 @@ int ln_forward_impl(const char* name, const float* a, const float* b, const floa
 
 struct BwdPlan {
     int W = 1, N = 0, G = 1;  // N == 0: block-per-row fallback
+    int waves = kBwdWaves;    // waves per workgroup
     int blocks = 0;
     size_t lds = 0;
 };
@@ -597,9 +599,16 @@ BwdPlan plan_bwd(int rows, int cols, bool vec4) {
             }
     }
     if (p.N) {
-        const int gpb = kBwdWaves / p.G;
+        // Rows of 4 waves with 4 vectors per lane (C around 3-4K) run one row
+        // group per 4-wave workgroup, 512 workgroups: no barrier couples two
+        // groups' rows ([32768, 4096] LN backward + residual 356.6 against
+        // 369.5 us with 8-wave workgroups of two groups; 1600-wide rows are
+        // slower that way, 28.2 against 27.1 us at [4096, 1600]).
+        p.waves = (p.G == 4 && p.N == 4) ? 4 : kBwdWaves;
+        const int maxb = p.waves == 4 ? 2 * MI_LN_BWD_MAX_BLOCKS : MI_LN_BWD_MAX_BLOCKS;
+        const int gpb = p.waves / p.G;
         const long long groups = (rows + gpb - 1) / gpb;
-        p.blocks = static_cast<int>(groups < MI_LN_BWD_MAX_BLOCKS ? groups : MI_LN_BWD_MAX_BLOCKS);
+        p.blocks = static_cast<int>(groups < maxb ? groups : maxb);
         p.lds = ln_bwd_flat_combine(gpb, cols)
                     ? static_cast<size_t>(gpb) * 2 * cols * sizeof(float)
                     : static_cast<size_t>(gpb / 2) * 2 * p.N * p.W * p.G * kWave * sizeof(float);
@@ -614,7 +623,15 @@ template <int W, int N, int G, bool ADD>
 void launch_bwd_group(const BwdPlan& p, hipStream_t st, const float* g, const float* x,
                       const float* m, const float* s, const float* gamma, float* gx, float* part,
                       int rows, int cols) {
-    hipLaunchKernelGGL((ln_bwd_group_kernel<W, N, G, ADD>), dim3(p.blocks),
+    if constexpr (G == 4 && N == 4) {
+        if (p.waves == 4) {
+            hipLaunchKernelGGL((ln_bwd_group_kernel<W, N, G, ADD, 4>), dim3(p.blocks),
+                               dim3(4 * kWave), p.lds, st, g, x, m, s, gamma, gx, part, rows,
+                               cols);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((ln_bwd_group_kernel<W, N, G, ADD, kBwdWaves>), dim3(p.blocks),
                        dim3(kBwdWaves * kWave), p.lds, st, g, x, m, s, gamma, gx, part, rows,
                        cols);
 }
