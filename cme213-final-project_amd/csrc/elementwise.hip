@@ -589,7 +589,11 @@ int launch_rowtile(const char* name, Op op, const float* bias, int rows, int col
                    hipStream_t st) {
     const int nv = cols / W;
     const unsigned long long nvec = static_cast<unsigned long long>(rows) * nv;
-    if (MI_FWD_FLAT && nvec < (1ull << 32)) {
+    // The flat kernel walks 32-bit vector indices: below 2^31 vectors,
+    // i + stride (stride <= MI_FLAT_MAX_GRID * kThreads) cannot wrap past
+    // 2^32 and restart the walk.  Larger tensors take the row bands, whose
+    // offsets are 64-bit.
+    if (MI_FWD_FLAT && nvec < (1ull << 31)) {
         long long grid = (static_cast<long long>(nvec) + kThreads - 1) / kThreads;
         if (grid > MI_FLAT_MAX_GRID) grid = MI_FLAT_MAX_GRID;
         hipLaunchKernelGGL((flatbias_kernel<W, Op>), dim3(static_cast<unsigned>(grid)),
