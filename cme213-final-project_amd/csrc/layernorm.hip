@@ -183,12 +183,13 @@ __global__ __launch_bounds__(kBlockThreads) void ln_fwd_block_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Backward, G waves per row, NWV waves per workgroup (kBwdWaves, or 4 for
-// 4-wave rows of 4 vectors per lane, see plan_bwd).
+// Backward, G waves per row, NWV waves per workgroup (kBwdWaves; 4 for
+// 4-wave rows of 4 vectors per lane; 16 for the residual-accumulate form
+// at one wave per row, see plan_bwd).
 // Dynamic LDS for the final combine of the GPB = NWV / G row groups:
 // GPB rows of 2*cols floats for the one-barrier combine (used for GPB >= 4
-// when that fits in 64 KB), else (GPB/2) slots of 2*N*W*64*G floats for the
-// binary tree.  With GPB = 2 the tree is a single step and measured faster
+// when that fits in 64 KB, 128 KB for 16 groups), else (GPB/2) slots of
+// 2*N*W*64*G floats for the binary tree.  With GPB = 2 the tree is a single step and measured faster
 // ([32768, 4096]: 457.3 against 458.5 us per LN fwd+bwd step).
 // ---------------------------------------------------------------------------
 #ifndef MI_LN_BWD_FLAT_LDS
@@ -196,9 +197,13 @@ __global__ __launch_bounds__(kBlockThreads) void ln_fwd_block_kernel(
 #endif
 constexpr size_t kFlatCombineLds = MI_LN_BWD_FLAT_LDS;
 
+__host__ __device__ constexpr size_t ln_bwd_flat_lds(int gpb) {
+    return gpb >= 16 ? 2 * kFlatCombineLds : kFlatCombineLds;
+}
+
 __host__ __device__ inline bool ln_bwd_flat_combine(int gpb, int cols) {
     return gpb >= 4 && static_cast<size_t>(gpb) * 2 * static_cast<size_t>(cols) *
-                               sizeof(float) <= kFlatCombineLds;
+                               sizeof(float) <= ln_bwd_flat_lds(gpb);
 }
 
 template <int W, int N, int G, bool ADD, int NWV>
@@ -364,7 +369,7 @@ __global__ __launch_bounds__(NWV * kWave) void ln_bwd_group_kernel(
     // Every width this instantiation handles (at most N*W*GT columns) may
     // fit the staging; then the choice needs no run-time test.
     constexpr bool kFlatAll = GPB >= 4 && static_cast<size_t>(GPB) * 2 * N * W * GT *
-                                              sizeof(float) <= kFlatCombineLds;
+                                              sizeof(float) <= ln_bwd_flat_lds(GPB);
     if (kFlatAll || ln_bwd_flat_combine(GPB, cols)) {
         // One barrier: every group stages its sums as a [2*cols] row
         // (dgamma then dbeta) in LDS, then each thread finishes a few
@@ -577,7 +582,7 @@ struct BwdPlan {
     size_t lds = 0;
 };
 
-BwdPlan plan_bwd(int rows, int cols, bool vec4) {
+BwdPlan plan_bwd(int rows, int cols, bool vec4, bool add) {
     BwdPlan p;
     p.W = vec4 ? 4 : 1;
     const int nv = cols / p.W;
@@ -604,7 +609,12 @@ BwdPlan plan_bwd(int rows, int cols, bool vec4) {
         // groups' rows ([32768, 4096] LN backward + residual 356.6 against
         // 369.5 us with 8-wave workgroups of two groups; 1600-wide rows are
         // slower that way, 28.2 against 27.1 us at [4096, 1600]).
-        p.waves = (p.G == 4 && p.N == 4) ? 4 : kBwdWaves;
+        // The residual-accumulate form at one wave per row and up to 3
+        // vectors per lane (C <= 768) runs 16-wave workgroups: with its
+        // third input stream, twice the waves per CU pay off (GPT-2-small
+        // block x12 2011.6 -> 1988.1 us), where the plain form is 0.7 us
+        // slower that way at [8192, 768].
+        p.waves = (p.G == 4 && p.N == 4) ? 4 : (add && p.G == 1 && p.N <= 3) ? 16 : kBwdWaves;
         const int maxb = p.waves == 4 ? 2 * MI_LN_BWD_MAX_BLOCKS : MI_LN_BWD_MAX_BLOCKS;
         const int gpb = p.waves / p.G;
         const long long groups = (rows + gpb - 1) / gpb;
@@ -623,6 +633,14 @@ template <int W, int N, int G, bool ADD>
 void launch_bwd_group(const BwdPlan& p, hipStream_t st, const float* g, const float* x,
                       const float* m, const float* s, const float* gamma, float* gx, float* part,
                       int rows, int cols) {
+    if constexpr (G == 1 && ADD && N <= 3) {
+        if (p.waves == 16) {
+            hipLaunchKernelGGL((ln_bwd_group_kernel<W, N, G, ADD, 16>), dim3(p.blocks),
+                               dim3(16 * kWave), p.lds, st, g, x, m, s, gamma, gx, part, rows,
+                               cols);
+            return;
+        }
+    }
     if constexpr (G == 4 && N == 4) {
         if (p.waves == 4) {
             hipLaunchKernelGGL((ln_bwd_group_kernel<W, N, G, ADD, 4>), dim3(p.blocks),
@@ -676,7 +694,7 @@ int ln_backward_impl(const char* name, const float* g, const float* x, const flo
         return set_error(MI_ERR_INVALID_ARG, "%s: NULL pointer", name);
     const bool vec4 = (cols % 4 == 0) && aligned16(g) && aligned16(x) && aligned16(gamma) &&
                       aligned16(gx);
-    const BwdPlan p = plan_bwd(rows, cols, vec4);
+    const BwdPlan p = plan_bwd(rows, cols, vec4, ADD);
     int err = MI_OK;
     char* ws = static_cast<char*>(workspace_get(bwd_workspace(p, cols), st, &err));
     if (!ws) return err;
@@ -704,10 +722,15 @@ extern "C" {
 
 size_t mi_layernorm_backward_workspace(int rows, int cols) {
     if (rows <= 0 || cols <= 0) return 0;
-    // The vec4 and scalar plans can differ; report the larger.
-    const size_t a = bwd_workspace(plan_bwd(rows, cols, cols % 4 == 0), cols);
-    const size_t b = bwd_workspace(plan_bwd(rows, cols, false), cols);
-    return a > b ? a : b;
+    // The vec4 and scalar plans, plain and residual-accumulate, can differ;
+    // report the largest.
+    size_t most = 0;
+    for (int add = 0; add < 2; ++add)
+        for (int v4 = 0; v4 < 2; ++v4) {
+            const size_t b = bwd_workspace(plan_bwd(rows, cols, v4 && cols % 4 == 0, add), cols);
+            if (b > most) most = b;
+        }
+    return most;
 }
 
 int mi_layernorm_forward(const float* x, const float* gamma, const float* beta, float* out,
