@@ -185,12 +185,13 @@ __global__ __launch_bounds__(kBlockThreads) void ln_fwd_block_kernel(
 // ---------------------------------------------------------------------------
 // Backward, G waves per row, NWV waves per workgroup (kBwdWaves; 4 for
 // 4-wave rows of 4 vectors per lane; 16 for the residual-accumulate form
-// at one wave per row, see plan_bwd).
+// at C <= 768 and at four waves per row up to C = 2048, see plan_bwd).
 // Dynamic LDS for the final combine of the GPB = NWV / G row groups:
 // GPB rows of 2*cols floats for the one-barrier combine (used for GPB >= 4
 // when that fits in 64 KB, 128 KB for 16 groups), else (GPB/2) slots of
-// 2*N*W*64*G floats for the binary tree.  With GPB = 2 the tree is a single step and measured faster
-// ([32768, 4096]: 457.3 against 458.5 us per LN fwd+bwd step).
+// 2*N*W*64*G floats for the binary tree.  With GPB = 2 the tree is a single
+// step and measured faster ([32768, 4096]: 457.3 against 458.5 us per LN
+// fwd+bwd step).
 // ---------------------------------------------------------------------------
 #ifndef MI_LN_BWD_FLAT_LDS
 #define MI_LN_BWD_FLAT_LDS (64 * 1024)
@@ -609,12 +610,15 @@ BwdPlan plan_bwd(int rows, int cols, bool vec4, bool add) {
         // groups' rows ([32768, 4096] LN backward + residual 356.6 against
         // 369.5 us with 8-wave workgroups of two groups; 1600-wide rows are
         // slower that way, 28.2 against 27.1 us at [4096, 1600]).
-        // The residual-accumulate form at one wave per row and up to 3
-        // vectors per lane (C <= 768) runs 16-wave workgroups: with its
-        // third input stream, twice the waves per CU pay off (GPT-2-small
-        // block x12 2011.6 -> 1988.1 us), where the plain form is 0.7 us
-        // slower that way at [8192, 768].
-        p.waves = (p.G == 4 && p.N == 4) ? 4 : (add && p.G == 1 && p.N <= 3) ? 16 : kBwdWaves;
+        // The residual-accumulate form runs 16-wave workgroups at one wave
+        // per row with up to 3 vectors per lane (C <= 768) and at four waves
+        // per row with up to 2 (C <= 2048): with its third input stream,
+        // twice the waves per CU pay off (GPT-2-small block x12 2011.6 ->
+        // 1988.1 us; GPT-2-XL-shaped block x48 8.80 -> 8.55 ms), where the
+        // plain form is 0.7 us slower that way at [8192, 768].
+        p.waves = (p.G == 4 && p.N == 4)                ? 4
+                  : (add && ((p.G == 1 && p.N <= 3) || (p.G == 4 && p.N <= 2))) ? 16
+                                                         : kBwdWaves;
         const int maxb = p.waves == 4 ? 2 * MI_LN_BWD_MAX_BLOCKS : MI_LN_BWD_MAX_BLOCKS;
         const int gpb = p.waves / p.G;
         const long long groups = (rows + gpb - 1) / gpb;
@@ -633,7 +637,7 @@ template <int W, int N, int G, bool ADD>
 void launch_bwd_group(const BwdPlan& p, hipStream_t st, const float* g, const float* x,
                       const float* m, const float* s, const float* gamma, float* gx, float* part,
                       int rows, int cols) {
-    if constexpr (G == 1 && ADD && N <= 3) {
+    if constexpr (ADD && ((G == 1 && N <= 3) || (G == 4 && N <= 2))) {
         if (p.waves == 16) {
             hipLaunchKernelGGL((ln_bwd_group_kernel<W, N, G, ADD, 16>), dim3(p.blocks),
                                dim3(16 * kWave), p.lds, st, g, x, m, s, gamma, gx, part, rows,

@@ -148,9 +148,17 @@ static void test_fusion_pairs() {
         residual_add(res_u.p, dx.p, res_u.p, n);  // in place, as the reference test does
         layernorm_backward_residual(grad.p, x.p, mean.p, inv.p, gam.p, res_f.p, dgf.p, dbf.p,
                                     rows, cols);
-        check(same_bits(res_u.get(), res_f.get()) && same_bits(dgu.get(), dgf.get()) &&
-                  same_bits(dbu.get(), dbf.get()),
-              "LN bwd+residual fused == unfused (bits)", max_abs_diff(res_u.get(), res_f.get()));
+        // The accumulated dx is row-local and identical; dgamma/dbeta are
+        // column sums whose (fixed) order follows each form's workgroup
+        // shape (the residual form runs 16-wave workgroups where the plain
+        // one runs 8), so they are held to the reference's criterion
+        // (FC/tests/test_fusion_benchmark.cu:276).
+        check(same_bits(res_u.get(), res_f.get()), "LN bwd+residual fused == unfused dx (bits)",
+              max_abs_diff(res_u.get(), res_f.get()));
+        const float dg_err = max_abs_diff(dgu.get(), dgf.get());
+        const float db_err = max_abs_diff(dbu.get(), dbf.get());
+        check(dg_err < 1e-4f, "LN bwd+residual dgamma (reference bound 1e-4)", dg_err);
+        check(db_err < 1e-4f, "LN bwd+residual dbeta (reference bound 1e-4)", db_err);
     }
     {  // bias + GELU: bias_add then GELU of the sum vs bias_gelu_forward; bwd repeatable
         const int rows = 512, cols = 3072, n = rows * cols;
