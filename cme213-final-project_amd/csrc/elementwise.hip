@@ -537,6 +537,42 @@ __global__ __launch_bounds__(kThreads) void flatbias_kernel(Op op, const float* 
     }
 }
 
+// The same walk with a stride that is a multiple of nv: every vector a
+// thread visits is in the same bias column, so the bias vector is loaded
+// once per thread and no division runs in the loop ([8192, 3072]: bias+ReLU
+// 33.1 -> 32.6 us, bias+GELU 33.1 -> 32.8 us, against 31.7 us for a plain
+// copy of the same bytes).
+template <int W, class Op>
+__global__ __launch_bounds__(kThreads) void flatcol_kernel(Op op, const float* __restrict__ bias,
+                                                           unsigned nvec, unsigned nv) {
+    const unsigned stride = gridDim.x * kThreads;
+    unsigned i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= nvec) return;
+    const fvec<W> b = vload<W>(bias, i % nv);
+    for (; i < nvec; i += stride) {
+        const typename Op::In in = op.load(i);
+        (void)op.apply(i, in, b);
+    }
+}
+
+// Workgroups of the column-fixed walk: a multiple of q = nv / gcd(nv,
+// kThreads), so that grid * kThreads is a multiple of nv, at most
+// MI_FLAT_MAX_GRID; 0 when q itself is larger.
+long long flatcol_grid(unsigned long long nvec, int nv) {
+    int a = nv, b = kThreads;
+    while (b != 0) {
+        const int t = a % b;
+        a = b;
+        b = t;
+    }
+    const long long q = nv / a;
+    if (q > MI_FLAT_MAX_GRID) return 0;
+    long long want = (static_cast<long long>(nvec) + kThreads - 1) / kThreads;
+    if (want > MI_FLAT_MAX_GRID) want = MI_FLAT_MAX_GRID;
+    const long long grid = (want + q - 1) / q * q;
+    return grid <= MI_FLAT_MAX_GRID ? grid : grid - q;
+}
+
 #ifndef MI_FWD_FLAT
 #define MI_FWD_FLAT 1
 #endif
@@ -593,7 +629,12 @@ int launch_rowtile(const char* name, Op op, const float* bias, int rows, int col
     // i + stride (stride <= MI_FLAT_MAX_GRID * kThreads) cannot wrap past
     // 2^32 and restart the walk.  Larger tensors take the row bands, whose
     // offsets are 64-bit.
-    if (MI_FWD_FLAT && nvec < (1ull << 31)) {
+    const long long cgrid = nvec < (1ull << 31) ? flatcol_grid(nvec, nv) : 0;
+    if (MI_FWD_FLAT && cgrid > 0) {
+        hipLaunchKernelGGL((flatcol_kernel<W, Op>), dim3(static_cast<unsigned>(cgrid)),
+                           dim3(kThreads), 0, st, op, bias, static_cast<unsigned>(nvec),
+                           static_cast<unsigned>(nv));
+    } else if (MI_FWD_FLAT && nvec < (1ull << 31)) {
         long long grid = (static_cast<long long>(nvec) + kThreads - 1) / kThreads;
         if (grid > MI_FLAT_MAX_GRID) grid = MI_FLAT_MAX_GRID;
         hipLaunchKernelGGL((flatbias_kernel<W, Op>), dim3(static_cast<unsigned>(grid)),
