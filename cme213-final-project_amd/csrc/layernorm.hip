@@ -74,8 +74,9 @@ __global__ __launch_bounds__(kFwdWaves * kWave) void ln_fwd_wave_kernel(
     }
     // With two plain rows of at most 4 vectors per lane, gamma and beta are
     // loaded once, behind the rows' loads, instead of per row after the
-    // statistics: the second row's loads then no longer wait behind the
-    // first row's stores (headline step 114.80 -> 114.54 us, five A/B
+    // statistics: the second row's gamma/beta loads, issued after the first
+    // row's stores, waited for those stores (the vector-memory counter
+    // retires in order) (headline step 114.80 -> 114.54 us, five A/B
     // pairs).  The residual form is slower that way (block x12 +25 us).
     constexpr bool kHoist = !RESID && R == 2 && N <= 4;
     fvec<W> gh[N], bh[N];
