@@ -18,7 +18,8 @@ Also reported on the same line:
                 from rocprofv3 FETCH_SIZE + WRITE_SIZE (profiles/), or null;
   cpu_baseline  the CPU oracle (a single-threaded C restatement of the
                 reference's CPU path) timed on this host on full-size steps
-                for about --cpu-seconds;
+                for about --cpu-seconds; `omp` beside it: the same oracle with
+                its OpenMP row loops on OMP_NUM_THREADS (else all) host cores;
   breakdown_us  average duration of each operation (HIP events).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
@@ -65,10 +66,28 @@ def cpu_baseline(inputs, seconds):
         times.append(time.perf_counter() - t0)
     times.sort()
     med = times[len(times) // 2]
+
+    # The row-parallel variant on the host cores (median of 5 steps).
+    ncpu = os.cpu_count() or 1
+    threads = max(1, min(int(os.environ.get("OMP_NUM_THREADS") or ncpu), ncpu))
+    O.set_threads(threads)
+    mt = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        y, m, s = O.layernorm_forward(x, gamma, beta)
+        O.layernorm_backward(dy, x, m, s, gamma)
+        O.bias_gelu_forward(h, bias)
+        O.gelu_backward_with_bias_backward(h, bias, dh)
+        mt.append(time.perf_counter() - t0)
+    O.set_threads(1)
+    mt.sort()
+    mmed = mt[len(mt) // 2]
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
             "rows_per_s": round(R / med, 1),
             "sample": f"{len(times)} full headline steps (LN [{R},{C}] fwd+bwd + bias+GELU "
-                      f"[{R},{F}] fwd+bwd), median {med * 1e3:.1f} ms/step, single thread"}
+                      f"[{R},{F}] fwd+bwd), median {med * 1e3:.1f} ms/step, single thread",
+            "omp": {"threads": threads, "nproc": ncpu, "value": round(nbytes / mmed / 1e9, 3),
+                    "ms_per_step": round(mmed * 1e3, 2), "sample": "median of 5 full steps"}}
 
 
 WORKLOADS = {
@@ -183,7 +202,8 @@ def main():
                 "~N(0,1), GELU pre-activation ~N(0,1.5), gamma=1+N(0,0.02), beta,bias~N(0,0.02)); "
                 "rotating buffer sets, backward on the previous step's set",
         "config": {"workload": WORKLOADS[args.workload], "bytes_per_step": step_bytes,
-                   "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2)},
+                   "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2),
+                   "seed": getattr(wl, "seed", None)},
     }
     # Token rows carried through the path per second (B*T rows per step; the
     # block sequences carry them through every layer).

@@ -83,6 +83,7 @@ class FwdBwd:
     def __init__(self, R=8192, C=768, F=3072, ln=True, gelu=True, sets=None, seed=20260):
         self.R, self.C, self.F = R, C, F
         self.ln, self.gelu = ln, gelu
+        self.seed = seed
         g = torch.Generator(device="cuda")
         g.manual_seed(seed)
         self.bytes = {}
@@ -167,6 +168,7 @@ class BlockSequence:
 
     def __init__(self, R, C, F, layers, seed=20263, shared_inputs=False):
         self.R, self.C, self.F, self.L = R, C, F, layers
+        self.seed = seed
         g = torch.Generator(device="cuda")
         g.manual_seed(seed)
         n_in = 1 if shared_inputs else layers
@@ -235,6 +237,7 @@ class Embedding:
 
     def __init__(self, V=50257, D=768, B=16, T=1024, sets=4, seed=20262):
         self.V, self.D, self.B, self.T = V, D, B, T
+        self.seed = seed
         g = torch.Generator(device="cuda")
         g.manual_seed(seed)
         self.wte = _randn((V, D), g, 0.02)
@@ -278,6 +281,7 @@ class CrossEntropy:
 
     def __init__(self, R=8192, V=50257, sets=2, seed=20268):
         self.R, self.V = R, V
+        self.seed = seed
         g = torch.Generator(device="cuda")
         g.manual_seed(seed)
         self.sets = []
@@ -311,6 +315,7 @@ class AdamStep:
 
     def __init__(self, n=124_439_808, seed=20269):
         self.n = n
+        self.seed = seed
         g = torch.Generator(device="cuda")
         g.manual_seed(seed)
         self.param = _randn((n,), g, 0.02)
@@ -341,6 +346,7 @@ class Relu16:
 
     def __init__(self, R=8192, F=3072, sets=4, seed=20270):
         self.R, self.F = R, F
+        self.seed = seed
         g = torch.Generator(device="cuda")
         g.manual_seed(seed)
         self.bias = _randn((F,), g, 0.02)
