@@ -16,8 +16,12 @@ pytestmark = pytest.mark.gpu
 # the wide sweep), the reference test shape, scalar / odd widths, widths past
 # the register-resident templates.  Tensors of 6M-16M elements with at least
 # 6144 rows take the two-rows-per-wave forward; (6161, 1022) covers it with
-# scalar loads and an odd row count (the last wave has one row).
+# scalar loads and an odd row count (the last wave has one row); (12289, 512)
+# and (24700, 255) cover its gamma/beta-once form (at most 4 vectors per
+# lane), with 16-byte and scalar loads, the first with an odd row count.
 SHAPES = [
+    (12289, 512, 20266),
+    (24700, 255, 20267),
     (4096, 768, 20260),
     (8192, 768, 20261),
     (4096, 1600, 20264),
