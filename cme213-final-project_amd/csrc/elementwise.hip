@@ -555,10 +555,14 @@ __global__ __launch_bounds__(kThreads) void flatcol_kernel(Op op, const float* _
     }
 }
 
-// Workgroups of the column-fixed walk: a multiple of q = nv / gcd(nv,
-// kThreads), so that grid * kThreads is a multiple of nv, at most
-// MI_FLAT_MAX_GRID; 0 when q itself is larger.
+// Workgroups of the column-fixed walk.  Up to MI_FLAT_MAX_GRID workgroups
+// every thread takes at most one vector, so any grid will do; beyond that
+// the grid is a multiple of q = nv / gcd(nv, kThreads), so that
+// grid * kThreads is a multiple of nv, at most MI_FLAT_MAX_GRID; 0 when q
+// itself is larger.
 long long flatcol_grid(unsigned long long nvec, int nv) {
+    const long long want = (static_cast<long long>(nvec) + kThreads - 1) / kThreads;
+    if (want <= MI_FLAT_MAX_GRID) return want;
     int a = nv, b = kThreads;
     while (b != 0) {
         const int t = a % b;
@@ -566,11 +570,7 @@ long long flatcol_grid(unsigned long long nvec, int nv) {
         b = t;
     }
     const long long q = nv / a;
-    if (q > MI_FLAT_MAX_GRID) return 0;
-    long long want = (static_cast<long long>(nvec) + kThreads - 1) / kThreads;
-    if (want > MI_FLAT_MAX_GRID) want = MI_FLAT_MAX_GRID;
-    const long long grid = (want + q - 1) / q * q;
-    return grid <= MI_FLAT_MAX_GRID ? grid : grid - q;
+    return q <= MI_FLAT_MAX_GRID ? MI_FLAT_MAX_GRID / q * q : 0;
 }
 
 #ifndef MI_FWD_FLAT

@@ -28,10 +28,11 @@ def test_residual_add_bit_exact_and_in_place(dev, n):
     assert_exact("in-place", host(A), ref)
 
 
-# (3, 16411): a prime width, whose column-fixed walk would need more than
-# the maximum grid, so the broadcast ops take the per-vector-column walk
+# (300, 16411): a prime width and more vectors than one walk step covers, so
+# a column-fixed walk would need more than the maximum grid and the
+# broadcast ops take the per-vector-column walk
 @pytest.mark.parametrize("rows,cols", [(8192, 768), (4096, 1600), (17, 33), (3, 1),
-                                       (70, 9001), (5, 40000), (3, 16411)])
+                                       (70, 9001), (5, 40000), (300, 16411)])
 def test_bias_and_relu_family(dev, rows, cols):
     note(f"bias/relu rows={rows} cols={cols}")
     r = np.random.default_rng(rows * 7 + cols)
@@ -79,7 +80,7 @@ def test_bias_and_relu_family(dev, rows, cols):
     (1, 3072, 6),
     (300, 9001, 7),       # wider than the row-band kernels: column-slice path
     (700, 3000, 8),       # rows not a multiple of the band count
-    (3, 16411, 9),        # prime width: the per-vector-column forward walk
+    (300, 16411, 9),      # prime width: the per-vector-column forward walk
 ])
 def test_bias_gelu_forward_backward(dev, rows, cols, seed):
     # GELU has no reference implementation; its reference is the published
