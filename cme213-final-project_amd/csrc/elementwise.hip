@@ -645,8 +645,9 @@ int launch_rowtile(const char* name, Op op, const float* bias, int rows, int col
         const int grid = rows < kFwdBands ? rows : kFwdBands;
         launch_band<W, Op, false>(b, grid, op, bias, nullptr, rows, nv, st);
     } else {
-        const int rps = (rows + kSlices - 1) / kSlices;
-        const dim3 grid((nv + kThreads - 1) / kThreads, (rows + rps - 1) / rps);
+        const int rps = static_cast<int>((static_cast<long long>(rows) + kSlices - 1) / kSlices);
+        const dim3 grid((nv + kThreads - 1) / kThreads,
+                        static_cast<unsigned>((static_cast<long long>(rows) + rps - 1) / rps));
         hipLaunchKernelGGL((colslice_kernel<W, Op, false>), grid, dim3(kThreads), 0, st, op, bias,
                            nullptr, rows, nv, rps);
     }
@@ -658,8 +659,8 @@ int launch_rowtile(const char* name, Op op, const float* bias, int rows, int col
 // only on the shape, so the summation order is fixed for a given shape.
 int plan_reduce_parts(int rows, int nv) {
     if (!band_fits(nv)) {
-        const int rps = (rows + kSlices - 1) / kSlices;
-        return (rows + rps - 1) / rps;
+        const int rps = static_cast<int>((static_cast<long long>(rows) + kSlices - 1) / kSlices);
+        return static_cast<int>((static_cast<long long>(rows) + rps - 1) / rps);
     }
     return rows < MI_REDUCE_TILES ? rows : MI_REDUCE_TILES;
 }
@@ -676,7 +677,7 @@ int launch_rowtile_reduce(const char* name, Op op, const float* bias, float* dbi
     if (band_fits(nv)) {
         launch_band<W, Op, true>(band_shape(nv), P, op, bias, part, rows, nv, st);
     } else {
-        const int rps = (rows + kSlices - 1) / kSlices;
+        const int rps = static_cast<int>((static_cast<long long>(rows) + kSlices - 1) / kSlices);
         const dim3 grid((nv + kThreads - 1) / kThreads, P);
         hipLaunchKernelGGL((colslice_kernel<W, Op, true>), grid, dim3(kThreads), 0, st, op, bias,
                            part, rows, nv, rps);

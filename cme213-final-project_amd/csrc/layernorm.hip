@@ -534,8 +534,8 @@ template <int W, int R, bool SAVE, bool RESID>
 void launch_fwd_wave(int n, hipStream_t st, const float* a, const float* b, const float* gamma,
                      const float* beta, float* ro, float* out, float* mo, float* so, int rows,
                      int cols, float eps) {
-    const int waves = (rows + R - 1) / R;
-    const dim3 grid((waves + kFwdWaves - 1) / kFwdWaves);
+    const long long waves = (static_cast<long long>(rows) + R - 1) / R;
+    const dim3 grid(static_cast<unsigned>((waves + kFwdWaves - 1) / kFwdWaves));
     const dim3 block(kFwdWaves * kWave);
 #define MI_LN_FWD_CASE(NN)                                                                     \
     case NN:                                                                                   \
@@ -638,7 +638,7 @@ BwdPlan plan_bwd(int rows, int cols, bool vec4, bool add) {
                                                          : kBwdWaves;
         const int maxb = p.waves == 4 ? 2 * MI_LN_BWD_MAX_BLOCKS : MI_LN_BWD_MAX_BLOCKS;
         const int gpb = p.waves / p.G;
-        const long long groups = (rows + gpb - 1) / gpb;
+        const long long groups = (static_cast<long long>(rows) + gpb - 1) / gpb;
         p.blocks = static_cast<int>(groups < maxb ? groups : maxb);
         p.lds = ln_bwd_flat_combine(gpb, cols)
                     ? static_cast<size_t>(gpb) * 2 * cols * sizeof(float)

@@ -233,7 +233,7 @@ template <int G, int K, bool CE>
 void launch_rows(int rows, int cols, hipStream_t st, const float* x, float* out, const int* tg,
                  float* losses, float scale) {
     constexpr int GPB = G < 4 ? 4 / G : 1;
-    const dim3 grid((rows + GPB - 1) / GPB);
+    const dim3 grid(static_cast<unsigned>((static_cast<long long>(rows) + GPB - 1) / GPB));
     hipLaunchKernelGGL((row_softmax_kernel<G, K, CE>), grid, dim3(sm_threads<G>()), 0, st, x, out,
                        rows, cols, tg, losses, scale);
 }
