@@ -81,6 +81,7 @@ _SIGS = {
         (c_int, [P, P, P, P, P, P, P, P, c_int, c_int, c_float, P]),
     "mi_layernorm_backward": (c_int, [P, P, P, P, P, P, P, P, c_int, c_int, P]),
     "mi_layernorm_backward_residual": (c_int, [P, P, P, P, P, P, P, P, c_int, c_int, P]),
+    "mi_layernorm_backward_noalloc": (c_int, [P, P, P, P, P, P, P, P, c_int, c_int, P]),
     # residual / bias / activations
     "mi_residual_add": (c_int, [P, P, P, c_longlong, P]),
     "mi_residual_add_with_bias": (c_int, [P, P, P, P, c_int, c_int, P]),
@@ -227,6 +228,19 @@ def layernorm_backward_residual(grad_out, x, mean, inv_std, gamma, grad_residual
     _check(lib.mi_layernorm_backward_residual(_f(grad_out), _f(x), _f(mean), _f(inv_std),
                                               _f(gamma), _f(grad_residual), _f(dgamma),
                                               _f(dbeta), rows, cols, _stream(stream)))
+
+
+# Static-scratch size of mi_layernorm_backward_noalloc (MI_LN_BWD_NOALLOC_MAX_BYTES).
+LN_BWD_NOALLOC_MAX_BYTES = 16 * 1024 * 1024 + 256
+
+
+def layernorm_backward_noalloc(grad_out, x, mean, inv_std, gamma, grad_x, dgamma, dbeta, rows,
+                               cols, stream=None):
+    """layernorm_backward without any device allocation: the partial rows use
+    the library's static per-device scratch (no reference counterpart)."""
+    _check(lib.mi_layernorm_backward_noalloc(_f(grad_out), _f(x), _f(mean), _f(inv_std),
+                                             _f(gamma), _f(grad_x), _f(dgamma), _f(dbeta), rows,
+                                             cols, _stream(stream)))
 
 
 # ----- residual / bias / activations (reference kernels.h:78-111) -------------

@@ -19,6 +19,7 @@
 //  * rows wider than the register-resident templates fall back to
 //    block-per-row kernels that stream the row from global memory.
 #include <climits>
+#include <mutex>
 
 #include "mi_common.hpp"
 
@@ -703,23 +704,36 @@ void dispatch_bwd_g(const BwdPlan& p, hipStream_t st, const float* g, const floa
 
 size_t bwd_workspace(const BwdPlan& p, int cols) { return colsum_bytes(p.blocks, 2 * cols); }
 
-template <bool ADD>
-int ln_backward_impl(const char* name, const float* g, const float* x, const float* m,
-                     const float* s, const float* gamma, float* gx, float* dgamma, float* dbeta,
-                     int rows, int cols, hipStream_t st) {
+// Argument checks shared by the backward entry points; *done is set when the
+// call is an empty no-op.
+int ln_backward_check(const char* name, const float* g, const float* x, const float* m,
+                      const float* s, const float* gamma, const float* gx, const float* dgamma,
+                      const float* dbeta, int rows, int cols, bool* done) {
+    *done = false;
     if (rows < 0 || cols <= 0)
         return set_error(MI_ERR_INVALID_ARG, "%s: invalid shape rows=%d cols=%d", name, rows,
                          cols);
-    if (rows == 0) return MI_OK;
+    if (rows == 0) {
+        *done = true;
+        return MI_OK;
+    }
     if (!g || !x || !m || !s || !gamma || !gx || !dgamma || !dbeta)
         return set_error(MI_ERR_INVALID_ARG, "%s: NULL pointer", name);
-    const bool vec4 = (cols % 4 == 0) && aligned16(g) && aligned16(x) && aligned16(gamma) &&
-                      aligned16(gx);
-    const BwdPlan p = plan_bwd(rows, cols, vec4, ADD);
-    int err = MI_OK;
-    char* ws = static_cast<char*>(workspace_get(bwd_workspace(p, cols), st, &err));
-    if (!ws) return err;
-    float* part = reinterpret_cast<float*>(ws + colsum_part_offset());
+    return MI_OK;
+}
+
+bool ln_backward_vec4(const float* g, const float* x, const float* gamma, const float* gx,
+                      int cols) {
+    return (cols % 4 == 0) && aligned16(g) && aligned16(x) && aligned16(gamma) && aligned16(gx);
+}
+
+// Launches the backward's main pass and its column-sum finalize with the
+// partial rows at `part` (at least p.blocks * 2 * cols floats).
+template <bool ADD>
+int ln_backward_launch(const char* name, const BwdPlan& p, const float* g, const float* x,
+                       const float* m, const float* s, const float* gamma, float* gx,
+                       float* dgamma, float* dbeta, float* part, int rows, int cols,
+                       hipStream_t st) {
     if (p.N) {
         if (p.W == 4)
             dispatch_bwd_g<4, ADD>(p, st, g, x, m, s, gamma, gx, part, rows, cols);
@@ -732,6 +746,60 @@ int ln_backward_impl(const char* name, const float* g, const float* x, const flo
     int rc = check_launch(name);
     if (rc != MI_OK) return rc;
     return launch_colsum_finalize(part, p.blocks, 2 * cols, dgamma, cols, dbeta, st);
+}
+
+template <bool ADD>
+int ln_backward_impl(const char* name, const float* g, const float* x, const float* m,
+                     const float* s, const float* gamma, float* gx, float* dgamma, float* dbeta,
+                     int rows, int cols, hipStream_t st) {
+    bool done = false;
+    if (int rc = ln_backward_check(name, g, x, m, s, gamma, gx, dgamma, dbeta, rows, cols, &done))
+        return rc;
+    if (done) return MI_OK;
+    const BwdPlan p = plan_bwd(rows, cols, ln_backward_vec4(g, x, gamma, gx, cols), ADD);
+    int err = MI_OK;
+    char* ws = static_cast<char*>(workspace_get(bwd_workspace(p, cols), st, &err));
+    if (!ws) return err;
+    float* part = reinterpret_cast<float*>(ws + colsum_part_offset());
+    return ln_backward_launch<ADD>(name, p, g, x, m, s, gamma, gx, dgamma, dbeta, part, rows,
+                                   cols, st);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free LayerNorm backward.  Its partial rows live in `scratch`, a
+// file-scope device array of fixed size (each device the library runs on
+// holds its own copy until the process ends).  Host code never passes the
+// array's name to a kernel: in host code that name is a host-side stand-in,
+// not a device address.  The device address of the current device's copy is
+// looked up once per device with hipGetSymbolAddress and cached.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = MI_LN_BWD_NOALLOC_MAX_BYTES;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+int scratch_address(const char* name, char** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return set_error(static_cast<int>(e), "%s: hipGetDevice failed: %s", name,
+                         hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxScratchDevices)
+        return set_error(MI_ERR_INVALID_ARG, "%s: device %d out of range", name, dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || ptr == nullptr)
+            return set_error(e != hipSuccess ? static_cast<int>(e) : MI_ERR_INVALID_ARG,
+                             "%s: hipGetSymbolAddress(scratch) failed: %s", name,
+                             hipGetErrorString(e));
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = static_cast<char*>(g_scratch_ptr[dev]);
+    return MI_OK;
 }
 
 }  // namespace
@@ -792,6 +860,31 @@ int mi_layernorm_backward_residual(const float* grad_out, const float* x, const 
     return ln_backward_impl<true>("mi_layernorm_backward_residual", grad_out, x, mean, inv_std,
                                   gamma, grad_residual, dgamma, dbeta, rows, cols,
                                   to_stream(stream));
+}
+
+int mi_layernorm_backward_noalloc(const float* grad_out, const float* x, const float* mean,
+                                  const float* inv_std, const float* gamma, float* grad_x,
+                                  float* dgamma, float* dbeta, int rows, int cols,
+                                  void* stream) {
+    const char* name = "mi_layernorm_backward_noalloc";
+    bool done = false;
+    if (int rc = ln_backward_check(name, grad_out, x, mean, inv_std, gamma, grad_x, dgamma, dbeta,
+                                   rows, cols, &done))
+        return rc;
+    if (done) return MI_OK;
+    const BwdPlan p =
+        plan_bwd(rows, cols, ln_backward_vec4(grad_out, x, gamma, grad_x, cols), false);
+    const size_t need = bwd_workspace(p, cols);
+    if (need > kScratchBytes)
+        return set_error(MI_ERR_INVALID_ARG,
+                         "%s: rows=%d cols=%d need %zu bytes of scratch, more than the static "
+                         "%zu; use mi_layernorm_backward",
+                         name, rows, cols, need, kScratchBytes);
+    char* base = nullptr;
+    if (int rc = scratch_address(name, &base)) return rc;
+    float* part = reinterpret_cast<float*>(base + colsum_part_offset());
+    return ln_backward_launch<false>(name, p, grad_out, x, mean, inv_std, gamma, grad_x, dgamma,
+                                     dbeta, part, rows, cols, to_stream(stream));
 }
 
 }  // extern "C"

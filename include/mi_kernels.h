@@ -98,6 +98,24 @@ int mi_layernorm_backward_residual(const float* grad_out, const float* x,
                                    float* dgamma, float* dbeta,
                                    int rows, int cols, void* stream);
 
+/* Allocation-free variant of mi_layernorm_backward (same arguments, same
+ * results bit for bit: it runs the same kernels).  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Its partial rows live in a static device array of
+ * MI_LN_BWD_NOALLOC_MAX_BYTES per device (held until the process ends)
+ * instead of the library workspace; the call makes no hipMalloc / hipFree.
+ * A shape whose partial rows need more (mi_layernorm_backward_workspace
+ * reports the need) is rejected with MI_ERR_INVALID_ARG.  Every call on a
+ * device shares that device's array: calls that overlap on one device (two
+ * streams, or two threads) race and must be serialised by the caller. */
+#define MI_LN_BWD_NOALLOC_MAX_BYTES ((size_t)16 * 1024 * 1024 + 256)
+int mi_layernorm_backward_noalloc(const float* grad_out, const float* x,
+                                  const float* mean, const float* inv_std,
+                                  const float* gamma, float* grad_x,
+                                  float* dgamma, float* dbeta,
+                                  int rows, int cols, void* stream);
+
 /* ----- residual / bias / ReLU ------------------------------------------- */
 
 /* out = a + b over n elements; out may alias a or b.  Replaces residual_add
