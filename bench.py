@@ -22,6 +22,11 @@ Also reported on the same line:
                 its OpenMP row loops on OMP_NUM_THREADS (else all) host cores;
   breakdown_us  average duration of each operation (HIP events).
 
+Before the timed region a bounded spin kernel (torch.cuda._sleep, about
+--hold-us) holds the stream while the host queues the first steps, so the
+start event is followed by queued work rather than by the host's launch
+latency; the spin itself precedes the start event.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 --workload picks another BASELINE config (ln, gelu, embedding, block12, xl48,
 wide), the softmax cross-entropy of the model loss (ce), the optimizer step
@@ -90,6 +95,22 @@ def cpu_baseline(inputs, seconds):
                     "ms_per_step": round(mmed * 1e3, 2), "sample": "median of 5 full steps"}}
 
 
+def hold_cycles_for(us):
+    """Spin-kernel cycle count that lasts about `us` microseconds, calibrated
+    with HIP events on this device (the spin counts shader clocks)."""
+    import torch
+    probe = 200000
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(probe)  # first launch loads the kernel
+    torch.cuda.synchronize()
+    e0.record()
+    torch.cuda._sleep(probe)
+    e1.record()
+    torch.cuda.synchronize()
+    per_us = probe / max(e0.elapsed_time(e1) * 1e3, 1.0)
+    return int(min(max(us * per_us, 1000), 50_000_000))
+
+
 WORKLOADS = {
     "headline": "LN fwd+bwd [8192,768] + bias+GELU fwd+bwd [8192,3072] (B=8, T=1024, C=768, F=4C)",
     "ln": "config 0: LN fwd+bwd [4096,768] (B=8, T=512)",
@@ -134,12 +155,16 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    # The first ~200 steps (about 25 ms of GPU work) run about 0.7 us per
-    # step slower than the steady state (113.4-113.6 against 112.7-112.9 us
-    # with 200, 1000 or 3000 warm-up steps), so the default warm-up covers
-    # them.
+    # Without the stream hold below, short runs read ~0.7-1.5 us per step
+    # slower than long ones (K = 20: 114.7-116.1 us against 113.2 us at
+    # K = 200 on one box): the GPU waits for the host's first launches after
+    # the start event.  With the hold, 5 and 200 warm-up steps agree within
+    # the run-to-run spread.
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--workload", default="headline", choices=sorted(WORKLOADS))
+    ap.add_argument("--hold-us", type=float, default=400.0,
+                    help="length of the spin that holds the stream before the timed region "
+                         "while the host queues the first steps (0: no hold)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
@@ -164,7 +189,17 @@ def main():
 
     # Timed region: exactly K steps between two events on the launch stream.
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    hold_cycles = hold_cycles_for(args.hold_us) if args.hold_us > 0 else 0
     torch.cuda.synchronize()
+    if hold_cycles:
+        # A bounded spin kernel holds the stream while the host queues the
+        # first steps, so the start event is followed by work that is already
+        # queued (the "blocking kernel" of GPU benchmark harnesses).  Without
+        # it the GPU idles after the start event until the host's first
+        # launches arrive, about 10 us, which at K = 20 steps reads as
+        # ~0.6 us per step of host latency.  The spin runs before the start
+        # event, outside the timed region.
+        torch.cuda._sleep(hold_cycles)
     start.record()
     for k in range(args.steps):
         wl.step(k)
@@ -207,7 +242,7 @@ def main():
                 "rotating buffer sets, backward on the previous step's set",
         "config": {"workload": WORKLOADS[args.workload], "bytes_per_step": step_bytes,
                    "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2),
-                   "seed": getattr(wl, "seed", None)},
+                   "seed": getattr(wl, "seed", None), "hold_us": args.hold_us},
     }
     # Token rows carried through the path per second (B*T rows per step; the
     # block sequences carry them through every layer).
