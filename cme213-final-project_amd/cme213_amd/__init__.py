@@ -71,6 +71,7 @@ _SIGS = {
     "mi_device_sync": (c_int, []),
     "mi_workspace_reserve": (c_int, [c_size_t]),
     "mi_workspace_bytes": (c_size_t, []),
+    "mi_workspace_release": (c_int, []),
     "mi_layernorm_backward_workspace": (c_size_t, [c_int, c_int]),
     "mi_bias_backward_workspace": (c_size_t, [c_int, c_int]),
     "mi_embedding_backward_workspace": (c_size_t, [c_int]),
@@ -190,6 +191,10 @@ def workspace_reserve(nbytes: int) -> None:
 
 def workspace_bytes() -> int:
     return lib.mi_workspace_bytes()
+
+
+def workspace_release() -> None:
+    _check(lib.mi_workspace_release())
 
 
 def device_sync() -> None:

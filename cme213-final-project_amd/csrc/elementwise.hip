@@ -55,9 +55,14 @@ constexpr int kUnroll = MI_EW_UNROLL;
 //   gelu'(u) = s + 2 u s (1 - s) z',  z' = sqrt(2/pi) (1 + 3*0.044715 u^2)
 //            = s (1 + 2 u (e s) z'),  since 1 - s = e s with e = e^{-2z}.
 // Neither form has the cancellation of 1 + tanh z for very negative u.
-// e^{-2z} is one v_exp_f32 (2^x) on -2 z log2(e), clamped to 2^126 so that
-// s and e*s stay finite (s then underflows towards 0, the correct limit);
-// 1 / (1 + e) is one v_rcp_f32.
+// e^{-2z} is one v_exp_f32 (2^x) on -2 z log2(e), its exponent clamped at
+// 126 so that e, s and e*s stay finite; 1 / (1 + e) is one v_rcp_f32.
+// Where the exponent reaches 126 (u below about -10, and u = -inf) gelu and
+// gelu' are below 1e-36 in magnitude and are returned as 0, their limit: u*s
+// with the clamped s = 2^-126 would grow like u (gelu(-1e38) = -1.2) and the
+// derivative like u^3.  Where e underflows to 0 (u above about 10.5, and
+// u = +inf) gelu' is exactly 1 = s, and the u*(e*s)*z' term, 0 * inf for
+// |u| > 1.8e19, is skipped.  NaN propagates through both.
 // ---------------------------------------------------------------------------
 // Folded constants: -2 z log2(e) = u * (kT0 + kT1 u^2), and
 // 2 z' = kD0 + kD1 u^2.
@@ -65,25 +70,31 @@ constexpr float kT0 = -2.302208198144325f;    // -2 * sqrt(2/pi) * log2(e)
 constexpr float kT1 = -0.1029432395800235f;   // -2 * sqrt(2/pi) * 0.044715 * log2(e)
 constexpr float kD0 = 1.5957691216057308f;    // 2 * sqrt(2/pi)
 constexpr float kD1 = 0.21406444881780076f;   // 2 * sqrt(2/pi) * 3 * 0.044715
+constexpr float kTMax = 126.0f;
 
 struct GeluTerms {
-    float s;  // 1 / (1 + e^{-2z})
-    float e;  // e^{-2z}
+    float s;     // 1 / (1 + e^{-2z})
+    float e;     // e^{-2z}, exponent clamped at kTMax
+    bool zero;   // the exponent reached kTMax: gelu and gelu' are 0
 };
 
 __device__ __forceinline__ GeluTerms gelu_terms(float u, float u2) {
-    const float t = fminf(u * fmaf(kT1, u2, kT0), 126.0f);
-    const float e = __builtin_amdgcn_exp2f(t);
-    return {__builtin_amdgcn_rcpf(1.0f + e), e};
+    const float t = u * fmaf(kT1, u2, kT0);
+    const float e = __builtin_amdgcn_exp2f(fminf(t, kTMax));
+    return {__builtin_amdgcn_rcpf(1.0f + e), e, t >= kTMax};
 }
 
-__device__ __forceinline__ float gelu_fwd(float u) { return u * gelu_terms(u, u * u).s; }
+__device__ __forceinline__ float gelu_fwd(float u) {
+    const GeluTerms g = gelu_terms(u, u * u);
+    return g.zero ? 0.0f : u * g.s;
+}
 
 __device__ __forceinline__ float gelu_grad(float u) {
     const float u2 = u * u;
     const GeluTerms g = gelu_terms(u, u2);
     // s (1 + 2 u (1 - s) z') with 1 - s = e s
-    return g.s * fmaf(u * (g.e * g.s), fmaf(kD1, u2, kD0), 1.0f);
+    const float d = g.s * fmaf(u * (g.e * g.s), fmaf(kD1, u2, kD0), 1.0f);
+    return g.zero ? 0.0f : (g.e == 0.0f ? g.s : d);
 }
 
 // ---------------------------------------------------------------------------
@@ -192,11 +203,11 @@ __global__ __launch_bounds__(1024) void rowband_kernel(Op op, const float* __res
     // carry no branches and the compiler waits for each row just before it
     // is used.
     using In = typename Op::In;
-    auto load_batch = [&](int r, In (&d)[U][NC]) {
+    auto load_batch = [&](unsigned r, In (&d)[U][NC]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int row = r + u * G;
-            const int rr = row < rows ? row : rows - 1;
+            const unsigned row = r + static_cast<unsigned>(u * G);
+            const int rr = row < static_cast<unsigned>(rows) ? static_cast<int>(row) : rows - 1;
 #pragma unroll
             for (int k = 0; k < NC; ++k) {
                 const int j = threadIdx.x + k * T;
@@ -209,15 +220,15 @@ __global__ __launch_bounds__(1024) void rowband_kernel(Op op, const float* __res
     // column-sum update are predicated.  The batch's inputs are consumed
     // unconditionally before the first store, so no load is sunk into a
     // predicated store and no wait has to cover a store.
-    auto run_batch = [&](int r, const In (&d)[U][NC]) {
+    auto run_batch = [&](unsigned r, const In (&d)[U][NC]) {
 #pragma unroll
         for (int u = 0; u < U; ++u)
 #pragma unroll
             for (int k = 0; k < NC; ++k) d[u][k].consume();
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int row = r + u * G;
-            const bool row_ok = row < rows;
+            const unsigned row = r + static_cast<unsigned>(u * G);
+            const bool row_ok = row < static_cast<unsigned>(rows);
             const size_t rb = static_cast<size_t>(row_ok ? row : 0) * nv;
 #pragma unroll
             for (int k = 0; k < NC; ++k) {
@@ -231,11 +242,15 @@ __global__ __launch_bounds__(1024) void rowband_kernel(Op op, const float* __res
             }
         }
     };
-    const int step = U * G;
-    const int first = blockIdx.x;
-    const int iters = first < rows ? (rows - first + step - 1) / step : 0;
+    // Row numbers and the trip count are unsigned: with rows near INT_MAX,
+    // the last batch's row numbers and rows - first + step - 1 exceed the
+    // int range (rows < 2^31 and step <= 2^20 keep them below 2^32).
+    const unsigned step = static_cast<unsigned>(U * G);
+    const unsigned first = blockIdx.x;
+    const unsigned iters = strided_trips(first, static_cast<unsigned>(rows), step);
     In A[U][NC];
-    for (int i = 0, r = first; i < iters; ++i, r += step) {
+    unsigned r = first;
+    for (unsigned i = 0; i < iters; ++i, r += step) {
         load_batch(r, A);
         run_batch(r, A);
     }

@@ -363,7 +363,8 @@ __global__ __launch_bounds__(NWV * kWave) void ln_bwd_group_kernel(
     // 290 against 269 us).
     constexpr int RF = (G > 1 && N <= 2) ? 2 : 1;
     const int first = blockIdx.x * GPB;
-    const int iters = first < rows ? (rows - first + stride - 1) / stride : 0;
+    const unsigned iters = strided_trips(static_cast<unsigned>(first), static_cast<unsigned>(rows),
+                                         static_cast<unsigned>(stride));
     // Row numbers are 64-bit: with rows near INT_MAX, row + r * stride may
     // exceed the int range for the masked tail.
     long long row = first + grp;
@@ -372,13 +373,13 @@ __global__ __launch_bounds__(NWV * kWave) void ln_bwd_group_kernel(
     // adds zeros.  With a possible zero-trip path the compiler kept gamma's
     // loads outstanding past the loop and waited for every store (vmcnt(0))
     // before the combine below.
-    int i = 0;
+    unsigned i = 0;
     do {
         RowIn cur[RF];
 #pragma unroll
         for (int r = 0; r < RF; ++r) load_row(row + r * stride, cur[r]);
 #pragma unroll
-        for (int r = 0; r < RF; ++r) process(cur[r], row + r * stride, (i + r) & 1);
+        for (int r = 0; r < RF; ++r) process(cur[r], row + r * stride, static_cast<int>((i + r) & 1u));
         i += RF;
         row += static_cast<long long>(RF) * stride;
     } while (i < iters);
@@ -476,7 +477,8 @@ __global__ __launch_bounds__(kBlockThreads) void ln_bwd_block_kernel(
         pg[c] = 0.0f;
         pb[c] = 0.0f;
     }
-    for (int row = blockIdx.x; row < rows; row += gridDim.x) {
+    // unsigned: row + gridDim.x may pass INT_MAX when rows is near it
+    for (unsigned row = blockIdx.x; row < static_cast<unsigned>(rows); row += gridDim.x) {
         const size_t off = static_cast<size_t>(row) * cols;
         const float mu = mean[row];
         const float is = rstd[row];

@@ -12,6 +12,7 @@
 #include <cstddef>
 #include <cstdint>
 
+#include "mi_index.hpp"
 #include "mi_kernels.h"
 
 namespace mi {

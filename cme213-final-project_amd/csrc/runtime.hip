@@ -6,16 +6,19 @@
 #include <mutex>
 
 #include "mi_common.hpp"
+#include "workspace_pool.hpp"
 
 namespace mi {
 
 namespace {
 thread_local char g_err[512] = "no error";
 
-constexpr int kMaxDevices = 64;
-std::mutex g_ws_mutex;
-void* g_ws_ptr[kMaxDevices] = {};
-size_t g_ws_bytes[kMaxDevices] = {};
+struct HipAlloc {
+    int alloc(void** p, size_t bytes) { return static_cast<int>(hipMalloc(p, bytes)); }
+    void free(void* p) { (void)hipFree(p); }
+};
+
+WorkspacePool<HipAlloc> g_ws;
 }  // namespace
 
 int set_error(int code, const char* fmt, ...) {
@@ -34,58 +37,44 @@ int check_launch(const char* what) {
     return MI_OK;
 }
 
-static int grow_workspace_locked(int dev, size_t bytes, hipStream_t stream) {
-    if (g_ws_bytes[dev] >= bytes) return MI_OK;
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (stream != nullptr && hipStreamIsCapturing(stream, &cs) == hipSuccess &&
-        cs != hipStreamCaptureStatusNone)
-        return set_error(MI_ERR_CAPTURE_ALLOC,
-                         "workspace of %zu bytes needed during graph capture "
-                         "(have %zu); call mi_workspace_reserve first",
-                         bytes, g_ws_bytes[dev]);
-    // Grow geometrically so a sequence of slightly larger shapes does not
-    // reallocate every call.  The old buffer may still be read by queued
-    // kernels, so drain the device before releasing it.
-    size_t want = round_up(bytes > 2 * g_ws_bytes[dev] ? bytes : 2 * g_ws_bytes[dev],
-                           size_t(1) << 20);
-    if (g_ws_ptr[dev] != nullptr) {
-        hipError_t e = hipDeviceSynchronize();
-        if (e != hipSuccess)
-            return set_error(static_cast<int>(e), "workspace: sync failed: %s",
-                             hipGetErrorString(e));
-        (void)hipFree(g_ws_ptr[dev]);
-        g_ws_ptr[dev] = nullptr;
-        g_ws_bytes[dev] = 0;
-    }
-    void* p = nullptr;
-    hipError_t e = hipMalloc(&p, want);
+static int current_device(int* dev) {
+    hipError_t e = hipGetDevice(dev);
     if (e != hipSuccess)
-        return set_error(static_cast<int>(e), "workspace: hipMalloc(%zu) failed: %s",
-                         want, hipGetErrorString(e));
-    g_ws_ptr[dev] = p;
-    g_ws_bytes[dev] = want;
+        return set_error(static_cast<int>(e), "hipGetDevice failed: %s", hipGetErrorString(e));
+    if (*dev < 0 || *dev >= WorkspacePool<HipAlloc>::kMaxDevices)
+        return set_error(MI_ERR_INVALID_ARG, "device %d out of range", *dev);
     return MI_OK;
 }
 
+// Growth never frees the buffer it replaces (queued kernels, a launch on
+// another thread or an instantiated graph may still use it) and never
+// synchronises: the old buffer is retired and kept until
+// mi_workspace_release().
 void* workspace_get(size_t bytes, hipStream_t stream, int* err) {
     int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) {
-        *err = set_error(static_cast<int>(e), "hipGetDevice failed: %s", hipGetErrorString(e));
-        return nullptr;
-    }
-    if (dev < 0 || dev >= kMaxDevices) {
-        *err = set_error(MI_ERR_INVALID_ARG, "device %d out of range", dev);
-        return nullptr;
-    }
-    std::lock_guard<std::mutex> lock(g_ws_mutex);
-    int rc = grow_workspace_locked(dev, bytes, stream);
-    if (rc != MI_OK) {
+    if (int rc = current_device(&dev)) {
         *err = rc;
         return nullptr;
     }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const bool capturing = stream != nullptr &&
+                           hipStreamIsCapturing(stream, &cs) == hipSuccess &&
+                           cs != hipStreamCaptureStatusNone;
+    int rc = MI_OK;
+    void* p = g_ws.get(dev, bytes, capturing, MI_ERR_CAPTURE_ALLOC, &rc);
+    if (p == nullptr) {
+        if (rc == MI_ERR_CAPTURE_ALLOC)
+            *err = set_error(MI_ERR_CAPTURE_ALLOC,
+                             "workspace of %zu bytes needed during graph capture (have %zu); "
+                             "call mi_workspace_reserve first",
+                             bytes, g_ws.bytes(dev));
+        else
+            *err = set_error(rc, "workspace: hipMalloc of %zu bytes failed: %s", bytes,
+                             hipGetErrorString(static_cast<hipError_t>(rc)));
+        return nullptr;
+    }
     *err = MI_OK;
-    return g_ws_ptr[dev];
+    return p;
 }
 
 }  // namespace mi
@@ -161,9 +150,18 @@ int mi_workspace_reserve(size_t bytes) {
 
 size_t mi_workspace_bytes(void) {
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= mi::kMaxDevices) return 0;
-    std::lock_guard<std::mutex> lock(mi::g_ws_mutex);
-    return mi::g_ws_bytes[dev];
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 ||
+        dev >= mi::WorkspacePool<mi::HipAlloc>::kMaxDevices)
+        return 0;
+    return mi::g_ws.bytes(dev);
+}
+
+int mi_workspace_release(void) {
+    int dev = 0;
+    if (int rc = mi::current_device(&dev)) return rc;
+    MI_HIP_TRY(hipDeviceSynchronize(), "mi_workspace_release: hipDeviceSynchronize");
+    mi::g_ws.release(dev);
+    return MI_OK;
 }
 
 }  // extern "C"

@@ -22,8 +22,11 @@
  * on identical inputs give identical bits.  The column reductions are
  * two-pass and use a library-owned device workspace; it is allocated on first
  * use (or by mi_workspace_reserve) and may not grow while the stream is being
- * captured into a graph.  Calls that share the workspace must not run
- * concurrently on different streams of the same device.
+ * captured into a graph.  Growth never frees or synchronises: the buffer it
+ * replaces stays allocated (queued kernels, a launch on another thread or an
+ * instantiated graph may still use it) until mi_workspace_release().  Calls
+ * that share the workspace must not run concurrently on different streams of
+ * the same device.
  */
 #ifndef MI_KERNELS_H
 #define MI_KERNELS_H
@@ -55,6 +58,11 @@ int mi_device_sync(void);
  * before graph capture).  mi_workspace_bytes() reports its current size. */
 int mi_workspace_reserve(size_t bytes);
 size_t mi_workspace_bytes(void);
+/* Synchronise the current device, then free its workspace buffers (the
+ * current one and every one a growth retired).  Only for a caller who will
+ * not replay a graph captured with workspace-using calls; the next call that
+ * needs a workspace allocates a new one. */
+int mi_workspace_release(void);
 /* Workspace an entry point needs for the given shape (bytes).  The token
  * embedding backward needs none: mi_embedding_backward_workspace returns 0. */
 size_t mi_layernorm_backward_workspace(int rows, int cols);

@@ -144,7 +144,31 @@ def test_gelu_special_values(dev):
     gin = host(GIN)[0]
     assert np.isfinite(gin).all()
     assert_bwd("gelu grad golden", gin, d["gin"].astype(np.float32))
-    assert_exact("dbias of one row is grad_in", host(DB), gin)
+    # dbias = 0 + grad_in (a -0.0 gradient adds to +0.0)
+    assert_exact("dbias of one row is grad_in", host(DB), gin + np.float32(0.0))
+
+
+def test_gelu_extreme_values(dev):
+    """Far tails and non-finite inputs: gelu(u) = 0 and gelu'(u) = 0 where
+    |gelu| < 1e-36 (u <= -10.5, -inf), gelu(u) = u and gelu'(u) = 1 where
+    the logistic factor is 1 in float (u >= 10.5, +inf), NaN stays NaN.
+    (The clamped exponent once gave gelu(-1e38) = -1.2 and gelu'(1e20) =
+    NaN.)"""
+    u = np.array([-np.inf, -3e38, -1e38, -1e20, -1e14, -1e12, -1e4, -20.0, -10.5,
+                  10.5, 20.0, 1e4, 1e12, 1e20, 1e38, 3e38, np.inf, np.nan], np.float32)
+    n = u.size
+    X = dev_t(u.reshape(1, n))
+    Bz = torch.zeros(n, device=dev)
+    Y = torch.empty_like(X)
+    M.bias_gelu_forward(X, Bz, Y, 1, n)
+    want_y = np.where(np.isnan(u), np.nan, np.where(u > 0, u, 0.0)).astype(np.float32)
+    assert np.array_equal(host(Y)[0], want_y, equal_nan=True), host(Y)[0]
+    GIN = torch.empty_like(X)
+    DB = torch.zeros(n, device=dev)
+    M.gelu_backward_with_bias_backward(X, Bz, torch.ones(1, n, device=dev), GIN, DB, 1, n)
+    want_g = np.where(np.isnan(u), np.nan, np.where(u > 0, 1.0, 0.0)).astype(np.float32)
+    assert np.array_equal(host(GIN)[0], want_g, equal_nan=True), host(GIN)[0]
+    assert np.array_equal(host(DB), want_g, equal_nan=True)
 
 
 def test_reduction_is_deterministic(dev):

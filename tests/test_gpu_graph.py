@@ -10,7 +10,7 @@ import torch
 
 import cme213_amd as M
 from gpu_util import host
-from tol import assert_exact
+from tol import assert_colsum, assert_exact
 
 pytestmark = pytest.mark.gpu
 
@@ -75,3 +75,80 @@ def test_graph_replays_match_the_eager_step(dev):
         torch.cuda.synchronize()
         for k, t in outputs.items():
             assert_exact(f"eager after replay {rep} {k}", host(t), ref[k])
+
+
+def test_graph_replays_after_workspace_growth(dev):
+    """A graph captured with workspace-using calls keeps working after an eager
+    call grows the workspace: the buffer baked into the graph is retired, not
+    freed, so replays neither fault nor corrupt memory handed out since."""
+    R, C, F = 1024, 768, 3072
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(2028)
+
+    def rn(*shape, scale=1.0):
+        return torch.randn(*shape, device=dev, generator=gen) * scale
+
+    x, dy, gamma = rn(R, C), rn(R, C), 1.0 + rn(C, scale=0.02)
+    h, dh, bias = rn(R, F, scale=1.5), rn(R, F), rn(F, scale=0.02)
+    mean, rstd = torch.empty(R, device=dev), torch.empty(R, device=dev)
+    M.layernorm_forward_save(x, gamma, torch.zeros(C, device=dev), torch.empty(R, C, device=dev),
+                             mean, rstd, R, C, 1e-5)
+    dx, gin = torch.empty(R, C, device=dev), torch.empty(R, F, device=dev)
+    dgamma, dbeta, dbias = (torch.empty(C, device=dev), torch.empty(C, device=dev),
+                            torch.empty(F, device=dev))
+    outputs = {"dx": dx, "dgamma": dgamma, "dbeta": dbeta, "grad_in": gin, "dbias": dbias}
+
+    def step():
+        for t in (dgamma, dbeta, dbias):
+            t.fill_(0.0)
+        M.layernorm_backward(dy, x, mean, rstd, gamma, dx, dgamma, dbeta, R, C)
+        M.gelu_backward_with_bias_backward(h, bias, dh, gin, dbias, R, F)
+
+    step()
+    torch.cuda.synchronize()
+    ref = {k: host(t) for k, t in outputs.items()}
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+
+    # An eager call that needs more workspace than the graph was captured with.
+    before = M.workspace_bytes()
+    rows, cols = 64, 1 << 16
+    while M.lib.mi_bias_backward_workspace(rows, cols) <= before:
+        cols *= 2
+    g = rn(rows, cols)
+    db = torch.zeros(cols, device=dev)
+    M.bias_backward(g, db, rows, cols)
+    torch.cuda.synchronize()
+    assert M.workspace_bytes() > before
+    assert_colsum("bias_backward after growth", host(db), host(g.double().sum(0)), host(g))
+    # Memory handed out after the growth must not be written by the replays.
+    filler = torch.full((before // 4 + 1024,), 3.0, device=dev)
+
+    for rep in range(3):
+        for t in outputs.values():
+            t.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        for k, t in outputs.items():
+            assert_exact(f"replay {rep} after growth {k}", host(t), ref[k])
+        step()
+        torch.cuda.synchronize()
+    assert bool((filler == 3.0).all())
+
+    # Releasing the workspace (no graph left to replay) and using it again.
+    del graph
+    torch.cuda.synchronize()
+    M.workspace_release()
+    assert M.workspace_bytes() == 0
+    step()
+    torch.cuda.synchronize()
+    for k, t in outputs.items():
+        assert_exact(f"eager after release {k}", host(t), ref[k])
