@@ -122,12 +122,14 @@ WORKLOADS = {
     "ce": "softmax cross-entropy of the model loss: logits [8192,50257] (B=8, T=1024, GPT-2 vocab)",
     "adam": "optimizer step (grad norm^2 + clip + Adam) over GPT-2 small's 124,439,808 parameters",
     "relu16": "fp16 activation storage: bias+ReLU to half fwd + half-mask ReLU bwd+dbias [8192,3072]",
+    "refshapes": "the reference's fused/unfused benchmarks at its shapes: LN fwd, residual+LN, LN "
+                 "bwd+residual [2048,128], bias+ReLU [2048,512] (cache-resident, as the reference)",
 }
 
 
 def make_workload(name):
     from cme213_amd.workloads import (AdamStep, BlockSequence, CrossEntropy, Embedding, FwdBwd,
-                                      Headline, Relu16)
+                                      Headline, RefShapes, Relu16)
     if name == "headline":
         return Headline()
     if name == "ln":
@@ -148,7 +150,43 @@ def make_workload(name):
         return AdamStep()
     if name == "relu16":
         return Relu16()
+    if name == "refshapes":
+        return RefShapes()
     raise SystemExit(f"unknown workload {name}; choose from {sorted(WORKLOADS)}")
+
+
+def refshapes(wl, args):
+    """The reference's cases, timed as the reference times them, by the C++
+    harness (RefShapes.run): one JSON line with every case beside the
+    reference's published numbers."""
+    us = wl.run(max(1, args.steps // 200))
+    cases = {}
+    tot_bytes, tot_us = 0, 0.0
+    for name in wl.CASES:
+        ref = wl.published(name)
+        cases[name] = {"us": round(us[name], 3),
+                       "gbs": round(wl.bytes[name] / (us[name] * 1e-6) / 1e9, 1),
+                       "bytes": wl.bytes[name], "reference_event_us": ref["event_us"],
+                       "reference_ncu_us": ref["ncu_us"]}
+        tot_bytes += wl.bytes[name]
+        tot_us += us[name]
+    for a in ("residual_ln", "ln_bwd_residual", "bias_relu"):
+        u, f = cases[a + "_unfused"], cases[a + "_fused"]
+        cases[a + "_speedup"] = {"mi355x": round(u["us"] / f["us"], 2),
+                                 "reference": round(u["reference_event_us"] /
+                                                    f["reference_event_us"], 2)}
+    print(json.dumps({
+        "metric": "refshapes achieved GB/s (reference byte model)",
+        "value": round(tot_bytes / (tot_us * 1e-6) / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": 200 * max(1, args.steps // 200), "warmup": 10,
+        "ms_per_step": round(tot_us * 1e-3, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (the reference's sin/cos fill_pattern inputs)",
+        "config": {"workload": WORKLOADS["refshapes"],
+                   "timing": "C++ loop through include/kernels.h on the per-thread stream, "
+                             "HIP events around 200-300 calls after 10 warm-up calls",
+                   "reference_hardware": "Quadro RTX 6000, 672 GB/s (context, not the same node)"},
+        "cases": cases}), flush=True)
 
 
 def main():
@@ -182,6 +220,9 @@ def main():
     wl = make_workload(args.workload)
     M.workspace_reserve(64 << 20)
     torch.cuda.synchronize()
+
+    if args.workload == "refshapes":
+        return refshapes(wl, args)
 
     for k in range(args.warmup):
         wl.step(k)

@@ -180,7 +180,48 @@ def _stream(stream):
     if stream is not None:
         return stream
     import torch
-    return torch.cuda.current_stream().cuda_stream
+    return torch._C._cuda_getCurrentRawStream(torch._C._cuda_getDevice())
+
+
+class Bound:
+    """One C-ABI call with its arguments converted once (device addresses,
+    sizes, scalars), for callers that issue the same call many times: a
+    call costs the ctypes dispatch alone, not the per-call tensor checks and
+    conversions of the wrapper functions.  The stream is torch's current one
+    at call time unless one was given.  The tensors are kept alive with the
+    binding.  Raises MIError on a non-zero status, like the wrappers."""
+
+    def __init__(self, name, *args, stream=None):
+        import torch
+        fn = getattr(lib, name)
+        types = _SIGS[name][1]
+        if len(args) != len(types) - 1:
+            raise TypeError(f"{name}: {len(types) - 1} arguments before the stream, "
+                            f"got {len(args)}")
+        self._keep = [a for a in args if isinstance(a, torch.Tensor)]
+        conv = []
+        for a, t in zip(args, types[:-1]):
+            if isinstance(a, torch.Tensor):
+                conv.append(c_void_p(_ptr(a)))
+            else:
+                conv.append(t(a) if a is not None else None)
+        self._fn, self._args, self._stream = fn, tuple(conv), stream
+        self.name = name
+
+    def __call__(self):
+        st = self._stream
+        if st is None:
+            import torch
+            st = torch._C._cuda_getCurrentRawStream(torch._C._cuda_getDevice())
+        rc = self._fn(*self._args, st)
+        if rc != MI_OK:
+            raise MIError(rc, last_error())
+
+
+def bind(name, *args, stream=None) -> Bound:
+    """Bound(name, *args): e.g. bind("mi_layernorm_backward", g, x, m, s, gamma,
+    dx, dgamma, dbeta, rows, cols)()."""
+    return Bound(name, *args, stream=stream)
 
 
 # ----- runtime ----------------------------------------------------------------
