@@ -86,3 +86,33 @@ def test_workspace_size_queries():
     assert M.lib.mi_embedding_backward_workspace(16384) == 0  # one kernel, LDS only
     assert M.lib.mi_layernorm_backward_workspace(0, 768) == 0
     assert M.lib.mi_cross_entropy_workspace(8192) >= 8192 * 4
+
+
+def test_bound_call_converts_once_and_raises_on_error():
+    # NULL device pointers with a valid shape: rejected on the host, no GPU call
+    f = M.bind("mi_layernorm_forward", 0, 0, 0, 0, 4, 8, 1e-5, stream=0)
+    with pytest.raises(M.MIError) as e:
+        f()
+    assert e.value.code == M.MI_ERR_INVALID_ARG and "NULL" in str(e.value)
+    # an empty shape is a successful no-op, repeatably
+    g = M.bind("mi_residual_add", 0, 0, 0, 0, stream=0)
+    g()
+    g()
+    # the argument count is checked against the C signature (stream excluded)
+    with pytest.raises(TypeError):
+        M.bind("mi_residual_add", 0, 0, 0)
+
+
+def test_noalloc_backward_rejects_oversized_shapes_on_the_host():
+    # 256 partial rows of 2 * 12288 floats need 24 MiB: more than the static
+    # scratch, rejected before any device call (the pointers are never used)
+    rows, cols = 4096, 12288
+    assert M.lib.mi_layernorm_backward_workspace(rows, cols) > M.LN_BWD_NOALLOC_MAX_BYTES
+    p = 256  # a non-NULL, 16-byte aligned stand-in address
+    rc = M.lib.mi_layernorm_backward_noalloc(p, p, p, p, p, p, p, p, rows, cols, None)
+    assert rc == M.MI_ERR_INVALID_ARG and "scratch" in M.last_error()
+    # the header's size and the Python constant agree
+    with open(M.HEADERS[0]) as f:
+        hdr = f.read()
+    assert "#define MI_LN_BWD_NOALLOC_MAX_BYTES ((size_t)16 * 1024 * 1024 + 256)" in hdr
+    assert M.LN_BWD_NOALLOC_MAX_BYTES == 16 * 1024 * 1024 + 256
