@@ -192,7 +192,9 @@ emb_bwd_owner_kernel(const int* __restrict__ ids, int n, int vocab, bool vec_ids
     __shared__ int s_next;
     __shared__ fvec<W> s_pacc[POS ? kOwnThreads : 1];  // first position rows, summed
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = static_cast<int>(threadIdx.x / kWave);
+    // Uniform over the wave; readfirstlane lets the compiler see that, so
+    // branches on it are scalar branches, not exec-masked ones.
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
     // gridDim.x is a power of two, so id % gridDim.x is a mask.
     const unsigned kmask = gridDim.x - 1u;
     const unsigned k = blockIdx.x;
@@ -347,7 +349,10 @@ emb_bwd_owner_kernel(const int* __restrict__ ids, int n, int vocab, bool vec_ids
     // Position gradient, first round: requests issued now, summed below.
     const long long pvec = POS ? static_cast<long long>(seq) * nv : 0;   // position vectors
     const long long pstride = static_cast<long long>(gridDim.x) * kOwnThreads;
-    const long long pv0 = static_cast<long long>(k) * kOwnThreads + threadIdx.x;
+    // A thread's first position vector, below kOwnMaxK * kOwnThreads = 2^18:
+    // 32 bits.  Held as a 64-bit value it was spilled to scratch, and its
+    // reload waited for every outstanding load.
+    const int pv0 = static_cast<int>(k) * kOwnThreads + wave * kWave + lane;
     const size_t bstride = static_cast<size_t>(seq) * nv;                // vectors per batch row
     // PRE batch rows of the first position vector are requested across the
     // id scan (7 for 2-3 column vectors per lane, 4 for one: more spills
@@ -394,29 +399,51 @@ emb_bwd_owner_kernel(const int* __restrict__ ids, int n, int vocab, bool vec_ids
         const long long wpos = base + static_cast<long long>(wave) * kOwnPer * kWave;
         int my[kOwnPer];
         unsigned bits = 0;
+        // Either the wave's whole span is in range with 16-byte aligned ids
+        // (one 16-byte load per group) or every id is a 4-byte load at a
+        // clamped position, masked after the load.  The choice is uniform
+        // over the wave and no load sits under a per-lane branch, so the
+        // waits that follow count these loads exactly: with per-lane
+        // branches the compiler waited for all but one of the position loads
+        // issued below before the first id was tested, which serialised
+        // them with the scan.
+        if (vec_ids && wpos + kOwnPer * kWave <= n) {
 #pragma unroll
-        for (int j = 0; j < kOwnGroups; ++j) {
-            const long long p4 = wpos + j * 4 * kWave + 4 * lane;
-            if (vec_ids && p4 + 3 < n) {
+            for (int j = 0; j < kOwnGroups; ++j) {
+                const long long p4 = wpos + j * 4 * kWave + 4 * lane;
                 const int4 v = *reinterpret_cast<const int4*>(ids + p4);
                 my[4 * j] = v.x;
                 my[4 * j + 1] = v.y;
                 my[4 * j + 2] = v.z;
                 my[4 * j + 3] = v.w;
-            } else {
+            }
+        } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) my[4 * j + e] = p4 + e < n ? ids[p4 + e] : -1;
+            for (int j = 0; j < kOwnGroups; ++j) {
+                const long long p4 = wpos + j * 4 * kWave + 4 * lane;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const long long p = p4 + e;
+                    const int v = ids[p < n ? p : n - 1];
+                    my[4 * j + e] = p < n ? v : -1;
+                }
             }
         }
         if constexpr (first) {
             // Issued after the id loads: loads complete in issue order, so
             // the scan can use its ids while these are still in flight.
-            if (pv0 < pvec) {
-                pacc = vload<W>(gpos, pv0);
+            // Unconditional loads, issued back to back on every lane: rows
+            // past the batch are clamped to its last row and lanes past the
+            // last position vector to that vector, and neither is added.
+            // With the loads under a per-lane branch the compiler's wait
+            // counts for the ids below had to allow for a path without
+            // them, and each id group then waited for one more of these.
+            const long long pvc = pv0 < pvec ? pv0 : pvec - 1;
+            pacc = vload<W>(gpos, static_cast<size_t>(pvc));
 #pragma unroll
-                for (int u = 0; u < PRE; ++u)
-                    pq[u] = u < batch ? sload<W>(g, u * bstride + pv0) : vzero<W>();
-            }
+            for (int u = 0; u < PRE; ++u)
+                pq[u] = sload<W>(g, static_cast<size_t>(u < batch ? u : batch - 1) * bstride +
+                                        static_cast<size_t>(pvc));
         }
 #pragma unroll
         for (int j = 0; j < kOwnGroups; ++j) {
