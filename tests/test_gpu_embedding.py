@@ -193,3 +193,38 @@ def test_embedding_backward_deterministic(dev):
     assert np.all(first[~touched] == 0)
     np.testing.assert_allclose(first.astype(np.float64).sum(axis=0),
                                g.astype(np.float64).sum(axis=0), rtol=1e-4, atol=1e-2)
+
+
+def _offset_dev(a, offset):
+    """Copy to the GPU starting `offset` elements into the allocation, so an
+    offset of 1 leaves the tensor 4-byte but not 16-byte aligned."""
+    flat = np.ascontiguousarray(a).reshape(-1)
+    buf = torch.empty(flat.size + offset, dtype=torch.from_numpy(flat[:1]).dtype, device="cuda:0")
+    view = buf[offset:]
+    view.copy_(torch.from_numpy(flat))
+    return view
+
+
+@pytest.mark.parametrize("V,D,B,T,id_off,g_off", [
+    (50257, 768, 16, 1024, 1, 0),   # config 2 with 4-byte aligned ids: every id a 4-byte load
+    (300, 64, 4, 1100, 1, 1),       # ids and gradient rows both off 16 bytes (scalar columns)
+    (1000, 128, 3, 333, 3, 0),      # ids 12 bytes in, ragged last id group
+    (17, 32, 1, 3, 1, 0),           # three tokens: fewer ids than one 16-byte load
+    (5, 16, 2, 1, 0, 1),            # two tokens, one position
+])
+def test_embedding_backward_unaligned_ids_and_rows(dev, V, D, B, T, id_off, g_off):
+    note(f"embedding unaligned V={V} D={D} B={B} T={T} id_off={id_off} g_off={g_off}")
+    _, _, ids, g = emb_inputs(V, D, B, T, 4242 + T)
+    ids[::5] = ids[0]              # repeated ids: runs longer than one entry
+    BT = B * T
+    r = np.random.default_rng(6)
+    dwte0 = r.standard_normal((V, D), dtype=np.float32)
+    dwpe0 = r.standard_normal((T, D), dtype=np.float32)
+    Ids, G = _offset_dev(ids, id_off), _offset_dev(g, g_off)
+    Dwte, Dwpe = dev_t(dwte0), dev_t(dwpe0)
+    M.embedding_pos_backward(G, Ids, Dwte, Dwpe, B, T, D, V)
+    assert_exact("fused dwte, unaligned", host(Dwte), O.embedding_backward(g, ids, dwte0))
+    assert_exact("fused dwpe, unaligned", host(Dwpe), O.pos_embedding_backward(g, dwpe0, B, T))
+    Twte = dev_t(dwte0)
+    M.embedding_backward(G, Ids, Twte, BT, D, V)
+    assert_exact("token dwte, unaligned", host(Twte), O.embedding_backward(g, ids, dwte0))
