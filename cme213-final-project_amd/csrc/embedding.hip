@@ -358,8 +358,8 @@ emb_bwd_owner_kernel(const int* __restrict__ ids, int n, int vocab, bool vec_ids
     // id scan (7 for 2-3 column vectors per lane, 4 for one: more spills
     // registers in the scan); with 4 column vectors per lane none fit, and the
     // position sums run after the token gradient alone.  The position
-    // bookkeeping kept across the token updates costs 2 spilled registers at
-    // 3 column vectors per lane, touched once before and once after them.
+    // bookkeeping kept across the token updates stays in registers (no
+    // instantiation spills).
     constexpr int PRE = !POS ? 0 : NCH == 1 ? 4 : NCH <= 3 ? kPosPre : 0;
     constexpr int NPQ = PRE > 0 ? PRE : 1;
     // Adds batch rows b0, b0 + 1, ... of position vector pv onto acc, in
