@@ -1,5 +1,5 @@
 """Host logic that needs no GPU, compiled with g++ under AddressSanitizer and
-UBSan (tests/cxx/host_checks.cpp): the 64-bit trip count of the row-band and
+UBSan (tests/cxx/host_checks.cpp): the unsigned trip count of the row-band and
 LayerNorm-backward row loops (csrc/mi_index.hpp) at row counts near INT_MAX,
 and the workspace pool (csrc/workspace_pool.hpp) under concurrent growth."""
 import os
