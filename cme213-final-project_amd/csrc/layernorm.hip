@@ -35,6 +35,20 @@ namespace {
 #define MI_LN_FWD_WAVES 4
 #endif
 constexpr int kFwdWaves = MI_LN_FWD_WAVES;  // waves per forward workgroup
+#ifndef MI_LN_FWD_GB_LDS
+#define MI_LN_FWD_GB_LDS 1
+#endif
+
+// gamma and beta staged in LDS once per workgroup, where a wave stores
+// before it needs them (the residual form, or a second row) and they are not
+// held in registers: read from global memory after a store, they waited for
+// that store (the vector-memory counter retires in order); LDS reads wait on
+// their own counter.  Block x12 1986-1987 -> 1972-1974 us, block x48
+// 8538-8544 -> 8395-8403 us, wide sweep 449.0-449.3 -> 447.8-448.2 us.
+template <int W, int N, int R, bool RESID>
+__host__ __device__ constexpr bool ln_fwd_gb_lds() {
+    return MI_LN_FWD_GB_LDS && W == 4 && !(!RESID && R == 2 && N <= 4) && (RESID || R > 1);
+}
 #ifndef MI_LN_BWD_WAVES
 #define MI_LN_BWD_WAVES 8
 #endif
@@ -53,7 +67,7 @@ __global__ __launch_bounds__(kFwdWaves * kWave) void ln_fwd_wave_kernel(
     float* __restrict__ mean_out, float* __restrict__ rstd_out, int rows, int cols, float eps) {
     const int lane = threadIdx.x & (kWave - 1);
     const int row0 = (blockIdx.x * kFwdWaves + static_cast<int>(threadIdx.x / kWave)) * R;
-    if (row0 >= rows) return;  // wave-uniform
+    if (!ln_fwd_gb_lds<W, N, R, RESID>() && row0 >= rows) return;  // wave-uniform
     const int nv = cols / W;
 
     fvec<W> v[R][N];
@@ -78,9 +92,24 @@ __global__ __launch_bounds__(kFwdWaves * kWave) void ln_fwd_wave_kernel(
     // statistics: the second row's gamma/beta loads, issued after the first
     // row's stores, waited for those stores (the vector-memory counter
     // retires in order) (headline step 114.80 -> 114.54 us, five A/B
-    // pairs).  The residual form is slower that way (block x12 +25 us).
+    // pairs).  The residual form is slower that way (block x12 +25 us); it,
+    // and two rows of more vectors, read gamma and beta from LDS instead,
+    // filled once per workgroup (ln_fwd_gb_lds).  Waves past the last row
+    // then stay to the barrier and store nothing.
     constexpr bool kHoist = !RESID && R == 2 && N <= 4;
+    constexpr bool kLds = ln_fwd_gb_lds<W, N, R, RESID>();
     fvec<W> gh[N], bh[N];
+    [[maybe_unused]] float* sgb = nullptr;
+    if constexpr (kLds) {
+        extern __shared__ __align__(16) float lds_gb[];
+        sgb = lds_gb;
+        const int nv2 = 2 * nv;
+        for (int i = threadIdx.x; i < nv2; i += kFwdWaves * kWave) {
+            const fvec<W> g = i < nv ? vload<W>(gamma, i) : vload<W>(beta, i - nv);
+            vstore<W>(sgb, i, g);
+        }
+        __syncthreads();
+    }
     if constexpr (kHoist) {
 #pragma unroll
         for (int k = 0; k < N; ++k) {
@@ -136,8 +165,8 @@ __global__ __launch_bounds__(kFwdWaves * kWave) void ln_fwd_wave_kernel(
         for (int k = 0; k < N; ++k) {
             const int j = lane + k * kWave;
             if (j < nv) {
-                const fvec<W> g = kHoist ? gh[k] : vload<W>(gamma, j);
-                const fvec<W> bt = kHoist ? bh[k] : vload<W>(beta, j);
+                const fvec<W> g = kHoist ? gh[k] : kLds ? vload<W>(sgb, j) : vload<W>(gamma, j);
+                const fvec<W> bt = kHoist ? bh[k] : kLds ? vload<W>(sgb, nv + j) : vload<W>(beta, j);
                 fvec<W> y;
 #pragma unroll
                 for (int e = 0; e < W; ++e)
@@ -542,7 +571,8 @@ void launch_fwd_wave(int n, hipStream_t st, const float* a, const float* b, cons
     const dim3 block(kFwdWaves * kWave);
 #define MI_LN_FWD_CASE(NN)                                                                     \
     case NN:                                                                                   \
-        hipLaunchKernelGGL((ln_fwd_wave_kernel<W, NN, R, SAVE, RESID>), grid, block, 0, st, a, \
+        hipLaunchKernelGGL((ln_fwd_wave_kernel<W, NN, R, SAVE, RESID>), grid, block,              \
+                           (ln_fwd_gb_lds<W, NN, R, RESID>() ? 2 * cols * sizeof(float) : 0), st, a, \
                            b, gamma, beta, ro, out, mo, so, rows, cols, eps);                  \
         break;
     switch (n) {
