@@ -75,7 +75,10 @@ def test_layernorm_forward_backward(dev, rows, cols, seed):
 
 
 @pytest.mark.parametrize("rows,cols,seed", [(4096, 768, 11), (1024, 1600, 12), (33, 65, 13),
-                                            (64, 4096, 14), (6145, 1600, 15)])
+                                            (64, 4096, 14), (6145, 1600, 15),
+                                            # partial last workgroups: waves past the last
+                                            # row still reach the gamma/beta staging barrier
+                                            (4097, 768, 16), (2, 768, 17)])
 def test_residual_layernorm_and_backward_residual(dev, rows, cols, seed):
     note(f"residual layernorm rows={rows} cols={cols}")
     x, gamma, beta, g = ln_inputs(rows, cols, seed)
