@@ -39,15 +39,17 @@ constexpr int kFwdWaves = MI_LN_FWD_WAVES;  // waves per forward workgroup
 #define MI_LN_FWD_GB_LDS 1
 #endif
 
-// gamma and beta staged in LDS once per workgroup, where a wave stores
-// before it needs them (the residual form, or a second row) and they are not
-// held in registers: read from global memory after a store, they waited for
-// that store (the vector-memory counter retires in order); LDS reads wait on
-// their own counter.  Block x12 1986-1987 -> 1972-1974 us, block x48
-// 8538-8544 -> 8395-8403 us, wide sweep 449.0-449.3 -> 447.8-448.2 us.
+// gamma and beta staged in LDS once per workgroup wherever a wave stores
+// before it needs them (the residual form, or a second row): read from
+// global memory after a store, they waited for that store (the
+// vector-memory counter retires in order); LDS reads wait on their own
+// counter.  Block x12 1986-1987 -> 1972-1974 us, block x48 8538-8544 ->
+// 8395-8403 us, wide sweep 449.0-449.3 -> 447.8-448.2 us; at the headline
+// shape (two rows of 3 vectors) it also beats holding them in registers
+// (LN forward 11.64-11.77 -> 11.45-11.56 us by events, five A/B rounds).
 template <int W, int N, int R, bool RESID>
 __host__ __device__ constexpr bool ln_fwd_gb_lds() {
-    return MI_LN_FWD_GB_LDS && W == 4 && !(!RESID && R == 2 && N <= 4) && (RESID || R > 1);
+    return MI_LN_FWD_GB_LDS && (RESID || R > 1);
 }
 #ifndef MI_LN_BWD_WAVES
 #define MI_LN_BWD_WAVES 8
@@ -87,18 +89,12 @@ __global__ __launch_bounds__(kFwdWaves * kWave) void ln_fwd_wave_kernel(
             }
         }
     }
-    // With two plain rows of at most 4 vectors per lane, gamma and beta are
-    // loaded once, behind the rows' loads, instead of per row after the
-    // statistics: the second row's gamma/beta loads, issued after the first
-    // row's stores, waited for those stores (the vector-memory counter
-    // retires in order) (headline step 114.80 -> 114.54 us, five A/B
-    // pairs).  The residual form is slower that way (block x12 +25 us); it,
-    // and two rows of more vectors, read gamma and beta from LDS instead,
-    // filled once per workgroup (ln_fwd_gb_lds).  Waves past the last row
-    // then stay to the barrier and store nothing.
-    constexpr bool kHoist = !RESID && R == 2 && N <= 4;
+    // Where a row's stores precede its gamma/beta reads (ln_fwd_gb_lds),
+    // gamma and beta come from LDS, filled once per workgroup; waves past
+    // the last row then stay to the barrier and store nothing.  Elsewhere
+    // (one plain row per wave) they are read from global memory after the
+    // statistics, with no store in front of them.
     constexpr bool kLds = ln_fwd_gb_lds<W, N, R, RESID>();
-    fvec<W> gh[N], bh[N];
     [[maybe_unused]] float* sgb = nullptr;
     if constexpr (kLds) {
         extern __shared__ __align__(16) float lds_gb[];
@@ -109,15 +105,6 @@ __global__ __launch_bounds__(kFwdWaves * kWave) void ln_fwd_wave_kernel(
             vstore<W>(sgb, i, g);
         }
         __syncthreads();
-    }
-    if constexpr (kHoist) {
-#pragma unroll
-        for (int k = 0; k < N; ++k) {
-            const int j = lane + k * kWave;
-            const int jj = j < nv ? j : nv - 1;
-            gh[k] = vload<W>(gamma, jj);
-            bh[k] = vload<W>(beta, jj);
-        }
     }
 
 #pragma unroll
@@ -165,8 +152,8 @@ __global__ __launch_bounds__(kFwdWaves * kWave) void ln_fwd_wave_kernel(
         for (int k = 0; k < N; ++k) {
             const int j = lane + k * kWave;
             if (j < nv) {
-                const fvec<W> g = kHoist ? gh[k] : kLds ? vload<W>(sgb, j) : vload<W>(gamma, j);
-                const fvec<W> bt = kHoist ? bh[k] : kLds ? vload<W>(sgb, nv + j) : vload<W>(beta, j);
+                const fvec<W> g = kLds ? vload<W>(sgb, j) : vload<W>(gamma, j);
+                const fvec<W> bt = kLds ? vload<W>(sgb, nv + j) : vload<W>(beta, j);
                 fvec<W> y;
 #pragma unroll
                 for (int e = 0; e < W; ++e)
