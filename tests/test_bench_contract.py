@@ -1,7 +1,8 @@
 """CPU checks of bench.py's contract: the algorithmic byte counts behind
-`value` and `roofline.achieved`, against the per-operation figures the
-survey of the reference states for each BASELINE config (MB = 1e6 B, two
-decimals), and the one-GPU rule (no GPU is touched)."""
+`value` and `roofline.achieved`, against per-operation figures worked out
+by hand from each benchmark config's interface tensors (read once, written
+once, accumulated outputs twice; MB = 1e6 B, two decimals), and the one-GPU
+rule (no GPU is touched)."""
 import os
 import subprocess
 import sys
