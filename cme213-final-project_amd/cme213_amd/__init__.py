@@ -71,6 +71,8 @@ _SIGS = {
     "mi_device_sync": (c_int, []),
     "mi_workspace_reserve": (c_int, [c_size_t]),
     "mi_workspace_bytes": (c_size_t, []),
+    "mi_workspace_reserve_stream": (c_int, [c_size_t, P]),
+    "mi_workspace_bytes_stream": (c_size_t, [P]),
     "mi_workspace_release": (c_int, []),
     "mi_layernorm_backward_workspace": (c_size_t, [c_int, c_int]),
     "mi_bias_backward_workspace": (c_size_t, [c_int, c_int]),

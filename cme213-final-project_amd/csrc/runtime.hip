@@ -46,6 +46,13 @@ static int current_device(int* dev) {
     return MI_OK;
 }
 
+// The workspace slot of a call on `stream`: the calling thread's own slot on
+// the per-thread default stream (two host threads' per-thread streams run
+// concurrently), else the device's shared slot.
+static int stream_slot(hipStream_t stream) {
+    return stream == hipStreamPerThread ? thread_slot() : WorkspacePool<HipAlloc>::kShared;
+}
+
 // Growth never frees the buffer it replaces (queued kernels, a launch on
 // another thread or an instantiated graph may still use it) and never
 // synchronises: the old buffer is retired and kept until
@@ -60,14 +67,16 @@ void* workspace_get(size_t bytes, hipStream_t stream, int* err) {
     const bool capturing = stream != nullptr &&
                            hipStreamIsCapturing(stream, &cs) == hipSuccess &&
                            cs != hipStreamCaptureStatusNone;
+    const int slot = stream_slot(stream);
     int rc = MI_OK;
-    void* p = g_ws.get(dev, bytes, capturing, MI_ERR_CAPTURE_ALLOC, &rc);
+    void* p = g_ws.get(dev, slot, bytes, capturing, MI_ERR_CAPTURE_ALLOC, &rc);
     if (p == nullptr) {
         if (rc == MI_ERR_CAPTURE_ALLOC)
             *err = set_error(MI_ERR_CAPTURE_ALLOC,
                              "workspace of %zu bytes needed during graph capture (have %zu); "
-                             "call mi_workspace_reserve first",
-                             bytes, g_ws.bytes(dev));
+                             "call mi_workspace_reserve (mi_workspace_reserve_stream for the "
+                             "per-thread stream) first",
+                             bytes, g_ws.bytes(dev, slot));
         else
             *err = set_error(rc, "workspace: hipMalloc of %zu bytes failed: %s", bytes,
                              hipGetErrorString(static_cast<hipError_t>(rc)));
@@ -148,12 +157,31 @@ int mi_workspace_reserve(size_t bytes) {
     return err;
 }
 
-size_t mi_workspace_bytes(void) {
+int mi_workspace_reserve_stream(size_t bytes, void* stream) {
+    hipStream_t st = mi::to_stream(stream);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (st != nullptr && hipStreamIsCapturing(st, &cs) == hipSuccess &&
+        cs != hipStreamCaptureStatusNone)
+        return set_error(MI_ERR_CAPTURE_ALLOC,
+                         "mi_workspace_reserve_stream: the stream is capturing; reserve before "
+                         "capture");
+    int err = MI_OK;
+    (void)mi::workspace_get(bytes, st, &err);
+    return err;
+}
+
+static size_t workspace_bytes_of(hipStream_t stream) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 ||
         dev >= mi::WorkspacePool<mi::HipAlloc>::kMaxDevices)
         return 0;
-    return mi::g_ws.bytes(dev);
+    return mi::g_ws.bytes(dev, mi::stream_slot(stream));
+}
+
+size_t mi_workspace_bytes(void) { return workspace_bytes_of(nullptr); }
+
+size_t mi_workspace_bytes_stream(void* stream) {
+    return workspace_bytes_of(mi::to_stream(stream));
 }
 
 int mi_workspace_release(void) {

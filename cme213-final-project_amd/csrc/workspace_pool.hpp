@@ -8,13 +8,32 @@
 // until release() is called by a caller who guarantees that no pending or
 // replayable work references any workspace buffer.  Geometric growth bounds
 // the retired memory by the size of the current buffer.
+//
+// Buffers are kept per (device, slot).  Slot kShared serves calls on
+// explicit streams and on the null stream: calls that share it must not run
+// concurrently on different streams of one device (the caller serialises
+// them, as one stream does).  Calls on the per-thread default stream
+// (hipStreamPerThread, the reference's `--default-stream per-thread`) run
+// concurrently when two host threads issue them, so each calling thread has
+// its own slot (thread_slot(), numbered from 1 on a thread's first use).  A
+// thread's slot stays allocated after the thread exits, until release().
 #pragma once
 
+#include <atomic>
 #include <cstddef>
+#include <map>
 #include <mutex>
 #include <vector>
 
 namespace mi {
+
+// The calling thread's workspace slot for per-thread-stream calls: a
+// process-wide number >= 1, fixed on the thread's first call.
+inline int thread_slot() {
+    static std::atomic<int> next{1};
+    thread_local const int slot = next.fetch_add(1, std::memory_order_relaxed);
+    return slot;
+}
 
 // Alloc provides
 //   int  alloc(void** p, size_t bytes);   // 0 on success, else an error code
@@ -23,17 +42,18 @@ template <class Alloc>
 class WorkspacePool {
   public:
     static constexpr int kMaxDevices = 64;
+    static constexpr int kShared = 0;
     static constexpr size_t kGrain = size_t(1) << 20;
 
     explicit WorkspacePool(Alloc a = Alloc()) : alloc_(a) {}
 
-    // Returns a buffer of at least `bytes` for device `dev`, growing the pool
-    // if needed (refused with `capture_err` while `capturing`).  On failure
-    // returns nullptr and stores the allocator's error (or capture_err) in
-    // *err.
-    void* get(int dev, size_t bytes, bool capturing, int capture_err, int* err) {
+    // Returns a buffer of at least `bytes` for (device `dev`, slot `slot`),
+    // growing that slot's buffer if needed (refused with `capture_err` while
+    // `capturing`).  On failure returns nullptr and stores the allocator's
+    // error (or capture_err) in *err.
+    void* get(int dev, int slot, size_t bytes, bool capturing, int capture_err, int* err) {
         std::lock_guard<std::mutex> lock(mu_);
-        Dev& d = dev_[dev];
+        Dev& d = at(dev, slot);
         if (d.cur != nullptr && d.bytes >= bytes) {
             *err = 0;
             return d.cur;
@@ -58,26 +78,23 @@ class WorkspacePool {
         return p;
     }
 
-    size_t bytes(int dev) {
+    size_t bytes(int dev, int slot = kShared) {
         std::lock_guard<std::mutex> lock(mu_);
-        return dev_[dev].bytes;
+        return at(dev, slot).bytes;
     }
 
-    size_t retired_count(int dev) {
+    size_t retired_count(int dev, int slot = kShared) {
         std::lock_guard<std::mutex> lock(mu_);
-        return dev_[dev].retired.size();
+        return at(dev, slot).retired.size();
     }
 
-    // Frees every buffer of `dev` (current and retired).  The caller
-    // guarantees that nothing pending or replayable references them.
+    // Frees every buffer of `dev` (current and retired, every slot).  The
+    // caller guarantees that nothing pending or replayable references them.
     void release(int dev) {
         std::lock_guard<std::mutex> lock(mu_);
-        Dev& d = dev_[dev];
-        for (void* p : d.retired) alloc_.free(p);
-        d.retired.clear();
-        if (d.cur != nullptr) alloc_.free(d.cur);
-        d.cur = nullptr;
-        d.bytes = 0;
+        drop(shared_[dev]);
+        for (auto& kv : threads_)
+            if (kv.first % kMaxDevices == dev) drop(kv.second);
     }
 
   private:
@@ -86,9 +103,25 @@ class WorkspacePool {
         size_t bytes = 0;
         std::vector<void*> retired;
     };
+
+    // std::map keeps references to its elements valid across inserts.
+    Dev& at(int dev, int slot) {
+        if (slot == kShared) return shared_[dev];
+        return threads_[static_cast<long long>(slot) * kMaxDevices + dev];
+    }
+
+    void drop(Dev& d) {
+        for (void* p : d.retired) alloc_.free(p);
+        d.retired.clear();
+        if (d.cur != nullptr) alloc_.free(d.cur);
+        d.cur = nullptr;
+        d.bytes = 0;
+    }
+
     Alloc alloc_;
     std::mutex mu_;
-    Dev dev_[kMaxDevices];
+    Dev shared_[kMaxDevices];
+    std::map<long long, Dev> threads_;
 };
 
 }  // namespace mi

@@ -24,9 +24,15 @@
  * use (or by mi_workspace_reserve) and may not grow while the stream is being
  * captured into a graph.  Growth never frees or synchronises: the buffer it
  * replaces stays allocated (queued kernels, a launch on another thread or an
- * instantiated graph may still use it) until mi_workspace_release().  Calls
- * that share the workspace must not run concurrently on different streams of
- * the same device.
+ * instantiated graph may still use it) until mi_workspace_release().
+ * Workspaces are kept per device and per slot.  Calls on an explicit stream
+ * or on the null stream share the device's slot: they must not run
+ * concurrently on different streams of the same device (one stream
+ * serialises them).  Calls on the per-thread default stream
+ * (hipStreamPerThread, which the include/kernels.h entry points use, as the
+ * reference's `--default-stream per-thread` build does) use a slot of the
+ * calling thread's own, so host threads may issue them concurrently.  A
+ * thread's slot is kept after the thread exits, until mi_workspace_release().
  */
 #ifndef MI_KERNELS_H
 #define MI_KERNELS_H
@@ -54,14 +60,21 @@ int mi_memcpy_d2h(void* dst, const void* src, size_t bytes);
 int mi_memset_zero(void* ptr, size_t bytes, void* stream);
 int mi_stream_sync(void* stream);
 int mi_device_sync(void);
-/* Grow the library workspace of the current device to >= bytes now (call
- * before graph capture).  mi_workspace_bytes() reports its current size. */
+/* Grow the shared workspace slot of the current device (the one calls on
+ * explicit streams and the null stream use) to >= bytes now (call before
+ * graph capture).  mi_workspace_bytes() reports its current size. */
 int mi_workspace_reserve(size_t bytes);
 size_t mi_workspace_bytes(void);
-/* Synchronise the current device, then free its workspace buffers (the
- * current one and every one a growth retired).  Only for a caller who will
- * not replay a graph captured with workspace-using calls; the next call that
- * needs a workspace allocates a new one. */
+/* The same for the slot that calls on `stream` from the calling thread use:
+ * the thread's own slot for hipStreamPerThread, else the shared slot.  For a
+ * caller that captures the per-thread stream into a graph.  Refused with
+ * MI_ERR_CAPTURE_ALLOC while `stream` is capturing. */
+int mi_workspace_reserve_stream(size_t bytes, void* stream);
+size_t mi_workspace_bytes_stream(void* stream);
+/* Synchronise the current device, then free its workspace buffers (every
+ * slot's current buffer and every one a growth retired).  Only for a caller
+ * who will not replay a graph captured with workspace-using calls; the next
+ * call that needs a workspace allocates a new one. */
 int mi_workspace_release(void);
 /* Workspace an entry point needs for the given shape (bytes).  The token
  * embedding backward needs none: mi_embedding_backward_workspace returns 0. */
@@ -111,8 +124,11 @@ int mi_layernorm_backward_residual(const float* grad_out, const float* x,
  * reference: it is for callers that cannot allocate device memory (code
  * under graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  Its partial rows live in a static device array of
- * MI_LN_BWD_NOALLOC_MAX_BYTES per device (held until the process ends)
- * instead of the library workspace; the call makes no hipMalloc / hipFree.
+ * MI_LN_BWD_NOALLOC_MAX_BYTES per device instead of the library workspace;
+ * the call makes no hipMalloc / hipFree.  The array is part of the
+ * library's code object, so every process that loads the library holds it
+ * (16 MiB + 256 B) on each device where the library's code is loaded, until
+ * the process ends, whether or not this entry point is ever called.
  * A shape whose partial rows need more (mi_layernorm_backward_workspace
  * reports the need) is rejected with MI_ERR_INVALID_ARG.  Every call on a
  * device shares that device's array: calls that overlap on one device (two

@@ -5,7 +5,13 @@
 //                           kernels use), one per line;
 //   pool                    drives mi::WorkspacePool from 8 threads with a
 //                           mock allocator and checks that no buffer handed
-//                           out is freed before release().
+//                           out is freed before release();
+//   slots                   8 threads, each with its own per-thread slot
+//                           (mi::thread_slot()) and the shared slot: a
+//                           thread's slot buffer is never another thread's,
+//                           the shared slot is one buffer for all, capture
+//                           refuses growth per slot, release() frees every
+//                           slot of the device and no other device's.
 #include <atomic>
 #include <chrono>
 #include <cstdio>
@@ -64,7 +70,8 @@ int pool_test() {
             for (int i = 0; i < 400; ++i) {
                 const size_t want = 1 + rng() % (48u << 20);
                 int err = -7;
-                unsigned char* p = static_cast<unsigned char*>(pool.get(dev, want, false, -2, &err));
+                unsigned char* p = static_cast<unsigned char*>(
+                    pool.get(dev, mi::WorkspacePool<MockAlloc>::kShared, want, false, -2, &err));
                 if (p == nullptr || err != 0) {
                     ++errors;
                     continue;
@@ -88,17 +95,88 @@ int pool_test() {
         return fail("a grown buffer was freed before release()");
     // capture: a request that fits is served, a larger one is refused
     int err = 0;
-    if (pool.get(dev, 1024, true, -2, &err) == nullptr || err != 0)
+    if (pool.get(dev, 0, 1024, true, -2, &err) == nullptr || err != 0)
         return fail("fitting request refused during capture");
-    if (pool.get(dev, cur + 1, true, -2, &err) != nullptr || err != -2)
+    if (pool.get(dev, 0, cur + 1, true, -2, &err) != nullptr || err != -2)
         return fail("growth allowed during capture");
     pool.release(dev);
     if (!g_live.empty()) return fail("release() left buffers allocated");
     if (pool.bytes(dev) != 0) return fail("release() left a current buffer");
     // usable again after release
-    if (pool.get(dev, 100, false, -2, &err) == nullptr) return fail("no buffer after release");
+    if (pool.get(dev, 0, 100, false, -2, &err) == nullptr) return fail("no buffer after release");
     pool.release(dev);
     std::printf("pool ok: %d allocations\n", g_allocs.load());
+    return 0;
+}
+
+int slots_test() {
+    using Pool = mi::WorkspacePool<MockAlloc>;
+    Pool pool;
+    const int dev = 5, other = 6;
+    constexpr int kThreads = 8;
+    std::atomic<int> errors{0};
+    std::mutex mu;
+    std::vector<std::set<void*>> own(kThreads);  // every buffer each thread's slot handed out
+    std::set<void*> shared;
+    std::vector<int> slot_of(kThreads, 0);
+    std::vector<std::thread> th;
+    for (int t = 0; t < kThreads; ++t) {
+        th.emplace_back([&, t] {
+            const int slot = mi::thread_slot();
+            if (slot < 1 || slot != mi::thread_slot()) ++errors;  // >= 1, fixed per thread
+            std::mt19937 rng(77 + t);
+            for (int i = 0; i < 200; ++i) {
+                const size_t want = 1 + rng() % (8u << 20);
+                int err = -7;
+                void* p = pool.get(dev, slot, want, false, -2, &err);
+                void* q = pool.get(dev, Pool::kShared, want / 2 + 1, false, -2, &err);
+                if (p == nullptr || q == nullptr || err != 0) {
+                    ++errors;
+                    continue;
+                }
+                std::memset(p, t, want);  // this thread's "kernel" fills its whole buffer
+                std::lock_guard<std::mutex> l(mu);
+                own[t].insert(p);
+                shared.insert(q);
+                slot_of[t] = slot;
+            }
+        });
+    }
+    for (auto& x : th) x.join();
+    if (errors) return fail("get or thread_slot misbehaved");
+    std::set<int> slots(slot_of.begin(), slot_of.end());
+    if (slots.size() != kThreads) return fail("two threads share a slot");
+    for (int a = 0; a < kThreads; ++a)
+        for (int b = a + 1; b < kThreads; ++b)
+            for (void* p : own[a])
+                if (own[b].count(p)) return fail("a slot buffer reached two threads");
+    for (int a = 0; a < kThreads; ++a)
+        for (void* p : own[a])
+            if (shared.count(p)) return fail("a thread's slot buffer is the shared one");
+    // the shared slot is one buffer at a time: all handed-out shared buffers
+    // are its current one or retired ones, geometric growth keeps them few
+    if (shared.size() > 8) return fail("shared slot grew too often");
+    // capture refuses growth per slot; a fitting request is served
+    int err = 0;
+    const int s0 = slot_of[0];
+    if (pool.get(dev, s0, pool.bytes(dev, s0) + 1, true, -2, &err) != nullptr || err != -2)
+        return fail("per-thread slot grew during capture");
+    if (pool.get(dev, s0, 16, true, -2, &err) == nullptr || err != 0)
+        return fail("fitting per-thread request refused during capture");
+    // another device's buffers survive this device's release
+    void* keep = pool.get(other, s0, 4096, false, -2, &err);
+    if (keep == nullptr) return fail("no buffer on the other device");
+    pool.release(dev);
+    if (pool.bytes(dev) != 0) return fail("release left the shared slot");
+    for (int s : slots)
+        if (pool.bytes(dev, s) != 0) return fail("release left a per-thread slot");
+    {
+        std::lock_guard<std::mutex> l(g_live_mu);
+        if (g_live.size() != 1 || !g_live.count(keep)) return fail("release freed the wrong buffers");
+    }
+    pool.release(other);
+    if (!g_live.empty()) return fail("buffers left after releasing both devices");
+    std::printf("slots ok: %zu slots\n", slots.size());
     return 0;
 }
 
@@ -106,6 +184,7 @@ int pool_test() {
 
 int main(int argc, char** argv) {
     if (argc >= 2 && std::strcmp(argv[1], "pool") == 0) return pool_test();
+    if (argc >= 2 && std::strcmp(argv[1], "slots") == 0) return slots_test();
     if (argc >= 2 && std::strcmp(argv[1], "trips") == 0) {
         for (int i = 2; i + 2 < argc; i += 3) {
             const long long first = std::atoll(argv[i]), n = std::atoll(argv[i + 1]),
@@ -116,6 +195,6 @@ int main(int argc, char** argv) {
         }
         return 0;
     }
-    std::fprintf(stderr, "usage: host_checks pool | trips FIRST N STEP ...\n");
+    std::fprintf(stderr, "usage: host_checks pool | slots | trips FIRST N STEP ...\n");
     return 2;
 }

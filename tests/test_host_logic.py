@@ -1,7 +1,8 @@
 """Host logic that needs no GPU, compiled with g++ under AddressSanitizer and
 UBSan (tests/cxx/host_checks.cpp): the unsigned trip count of the row-band and
 LayerNorm-backward row loops (csrc/mi_index.hpp) at row counts near INT_MAX,
-and the workspace pool (csrc/workspace_pool.hpp) under concurrent growth."""
+and the workspace pool (csrc/workspace_pool.hpp) under concurrent growth and
+with per-thread slots (the per-thread default stream's keying)."""
 import os
 import shutil
 import subprocess
@@ -48,3 +49,10 @@ def test_workspace_pool_never_frees_a_handed_out_buffer(exe):
     r = subprocess.run([exe, "pool"], capture_output=True, text=True, env=env, timeout=300)
     assert r.returncode == 0, r.stderr[-2000:]
     assert "pool ok" in r.stdout
+
+
+def test_workspace_pool_per_thread_slots(exe):
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0")
+    r = subprocess.run([exe, "slots"], capture_output=True, text=True, env=env, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert "slots ok: 8 slots" in r.stdout
