@@ -20,7 +20,13 @@ Also reported on the same line:
                 reference's CPU path) timed on this host on full-size steps
                 for about --cpu-seconds; `omp` beside it: the same oracle with
                 its OpenMP row loops on OMP_NUM_THREADS (else all) host cores;
-  breakdown_us  average duration of each operation (HIP events).
+  breakdown_us  average duration of each operation (HIP events);
+  configs       every other BASELINE config (0: ln, 1: gelu, 2: embedding,
+                3: block12, 4: xl48 and wide), each timed in the same process
+                after the headline's timed region, with its own rotating
+                buffers, warm-up and step count: time per step, GB/s, % of
+                peak and the time at 70% of peak (BASELINE.md section 2's
+                target where it states one); --no-configs skips it.
 
 Before the timed region a bounded spin kernel (torch.cuda._sleep, about
 --hold-us) holds the stream while the host queues the first steps, so the
@@ -97,8 +103,13 @@ def cpu_baseline(inputs, seconds):
 
 def hold_cycles_for(us):
     """Spin-kernel cycle count that lasts about `us` microseconds, calibrated
-    with HIP events on this device (the spin counts shader clocks)."""
+    with HIP events on this device (the spin counts shader clocks); 0 when
+    this torch build has no spin kernel (torch.cuda._sleep is private)."""
     import torch
+    if not hasattr(torch.cuda, "_sleep"):
+        print("bench.py: torch.cuda._sleep is missing in this torch build; the timed region "
+              "runs without the stream hold (--hold-us 0)", file=sys.stderr)
+        return 0
     probe = 200000
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda._sleep(probe)  # first launch loads the kernel
@@ -122,14 +133,33 @@ WORKLOADS = {
     "ce": "softmax cross-entropy of the model loss: logits [8192,50257] (B=8, T=1024, GPT-2 vocab)",
     "adam": "optimizer step (grad norm^2 + clip + Adam) over GPT-2 small's 124,439,808 parameters",
     "relu16": "fp16 activation storage: bias+ReLU to half fwd + half-mask ReLU bwd+dbias [8192,3072]",
-    "refshapes": "the reference's fused/unfused benchmarks at its shapes: LN fwd, residual+LN, LN "
-                 "bwd+residual [2048,128], bias+ReLU [2048,512] (cache-resident, as the reference)",
+    "floor": "launch and streaming floors: empty-kernel chains; config 0's and the headline's "
+             "bytes as plain streaming kernels in their own launch structure, beside the "
+             "library's steps (C++ harness)",
+    "refshapes": "the reference's kernel benchmarks at its shapes: fused/unfused LN fwd, residual+LN, "
+                 "LN bwd+residual [2048,128], bias+ReLU [2048,512]; the LN forward grids of "
+                 "benchmark_all.cu and deep_profile.cu (cache-resident, as the reference)",
 }
+
+
+# The configs reported beside the headline, in the
+# order BASELINE.md section 2 lists them: (key, workload, warm-up steps, timed
+# steps, BASELINE.md's stated target in us or None where it says "reported").
+CONFIG_SUITE = [
+    ("config0_ln", "ln", 20, 100, 11.3),
+    ("config1_gelu", "gelu", 20, 100, 89.9),
+    ("config2_embedding", "embedding", 20, 100, None),
+    ("config3_block12", "block12", 3, 20, 1940.0),
+    ("config4_xl48", "xl48", 2, 10, None),
+    ("config4_wide", "wide", 5, 50, None),
+]
 
 
 def make_workload(name):
     from cme213_amd.workloads import (AdamStep, BlockSequence, CrossEntropy, Embedding, FwdBwd,
                                       Headline, RefShapes, Relu16)
+    if name == "floor":
+        return None
     if name == "headline":
         return Headline()
     if name == "ln":
@@ -158,18 +188,24 @@ def make_workload(name):
 def refshapes(wl, args):
     """The reference's cases, timed as the reference times them, by the C++
     harness (RefShapes.run): one JSON line with every case beside the
-    reference's published numbers."""
-    us = wl.run(max(1, args.steps // 200))
+    reference's published numbers.  Cases run different numbers of calls
+    (their own loops), so each case reports its own count; `value` is the
+    byte-weighted rate over all cases (sum of bytes / sum of per-call times)."""
+    res = wl.run(max(1, args.steps // 200))
     cases = {}
     tot_bytes, tot_us = 0, 0.0
-    for name in wl.CASES:
+    for name in wl.names():
+        us, calls = res[name]["us"], res[name]["calls"]
         ref = wl.published(name)
-        cases[name] = {"us": round(us[name], 3),
-                       "gbs": round(wl.bytes[name] / (us[name] * 1e-6) / 1e9, 1),
-                       "bytes": wl.bytes[name], "reference_event_us": ref["event_us"],
+        cases[name] = {"us": round(us, 3), "calls": calls,
+                       "gbs": round(wl.bytes[name] / (us * 1e-6) / 1e9, 1),
+                       "bytes": wl.bytes[name],
+                       "reference_event_us": ref["event_us"],
                        "reference_ncu_us": ref["ncu_us"]}
+        if "event_us_other_run" in ref:
+            cases[name]["reference_event_us_other_run"] = ref["event_us_other_run"]
         tot_bytes += wl.bytes[name]
-        tot_us += us[name]
+        tot_us += us
     for a in ("residual_ln", "ln_bwd_residual", "bias_relu"):
         u, f = cases[a + "_unfused"], cases[a + "_fused"]
         cases[a + "_speedup"] = {"mi355x": round(u["us"] / f["us"], 2),
@@ -178,15 +214,103 @@ def refshapes(wl, args):
     print(json.dumps({
         "metric": "refshapes achieved GB/s (reference byte model)",
         "value": round(tot_bytes / (tot_us * 1e-6) / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
-        "steps": 200 * max(1, args.steps // 200), "warmup": 10,
-        "ms_per_step": round(tot_us * 1e-3, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f32",
-        "data": "synthetic (the reference's sin/cos fill_pattern inputs)",
+        "steps": None, "warmup": None, "us_per_call_sum": round(tot_us, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (the reference harnesses' inputs: the fusion benchmark's sin/cos "
+                "fill_pattern; srand(42) rand()/RAND_MAX - 0.5 for the LayerNorm grids)",
         "config": {"workload": WORKLOADS["refshapes"],
-                   "timing": "C++ loop through include/kernels.h on the per-thread stream, "
-                             "HIP events around 200-300 calls after 10 warm-up calls",
+                   "timing": "C++ loop through include/kernels.h on the per-thread stream, HIP "
+                             "events around each case's own call count (cases.*.calls) after "
+                             "its own warm-up (10, or 20 for the deep_profile cases)",
                    "reference_hardware": "Quadro RTX 6000, 672 GB/s (context, not the same node)"},
         "cases": cases}), flush=True)
+
+
+def floor(args):
+    """The launch and streaming floors of bench/launch_floor.cpp (one JSON
+    line): the cost of a dependent launch from chains of 1-3 empty kernels,
+    and the config-0 and headline steps beside the same bytes moved by plain
+    streaming kernels in the same launch structure."""
+    import subprocess
+    exe = os.path.join(ROOT, "cme213-final-project_amd", "launch_floor")
+    out = subprocess.run([exe, str(max(1, args.steps // 200))], capture_output=True, text=True,
+                         check=True, timeout=300).stdout
+    t = json.loads(out.strip().splitlines()[-1])
+    per_launch = {str(g): round((t[f"empty_chain_3x{g}"] - t[f"empty_chain_1x{g}"]) / 2, 3)
+                  for g in (48, 256, 2048, 16384)}
+    from cme213_amd.workloads import headline_bytes, ln_bwd_bytes, ln_fwd_bytes
+    c0 = ln_fwd_bytes(4096, 768) + ln_bwd_bytes(4096, 768)
+    hb = sum(headline_bytes().values())
+    print(json.dumps({
+        "metric": "config-0 step time against its plain-kernel floor", "value":
+            round(t["config0_step"], 3), "unit": "us", "n_gpus": 1, "steps": None,
+        "warmup": 20, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "constant-filled buffers, rotating sets (>= 1 GB between reuses)",
+        "config": {"workload": WORKLOADS["floor"]},
+        "us": {k: round(v, 3) for k, v in t.items()},
+        "dependent_launch_us_by_workgroups": per_launch,
+        "config0": {"bytes": c0, "floor_us": round(t["config0_floor"], 3),
+                    "step_us": round(t["config0_step"], 3),
+                    "step_minus_floor_us": round(t["config0_step"] - t["config0_floor"], 3),
+                    "us_at_70pct": round(c0 / (0.7 * PEAK_HBM_GBS * 1e9) * 1e6, 2)},
+        "headline": {"bytes": hb, "floor_us": round(t["headline_floor"], 3),
+                     "step_us": round(t["headline_step"], 3),
+                     "floor_pct_of_peak": round(100 * hb / (t["headline_floor"] * 1e-6) / 1e9 /
+                                                PEAK_HBM_GBS, 2),
+                     "step_pct_of_peak": round(100 * hb / (t["headline_step"] * 1e-6) / 1e9 /
+                                               PEAK_HBM_GBS, 2)}}), flush=True)
+
+
+def timed_steps(wl, warmup, steps, hold_cycles):
+    """W untimed steps, then exactly K steps between two events on the launch
+    stream (the spin kernel, when given, holds the stream before the start
+    event while the host queues the first steps).  Returns ms per step."""
+    import torch
+    for k in range(warmup):
+        wl.step(k)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if hold_cycles:
+        # A bounded spin kernel holds the stream while the host queues the
+        # first steps, so the start event is followed by work that is already
+        # queued (the "blocking kernel" of GPU benchmark harnesses).  Without
+        # it the GPU idles after the start event until the host's first
+        # launches arrive, about 10 us, which at K = 20 steps reads as
+        # ~0.6 us per step of host latency.  The spin runs before the start
+        # event, outside the timed region.
+        torch.cuda._sleep(hold_cycles)
+    start.record()
+    for k in range(steps):
+        wl.step(warmup + k)
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def config_suite(hold_cycles):
+    """Each BASELINE config's workload, timed like the headline (its own
+    rotating buffers, warm-up, spin hold and event-bracketed steps), one
+    after the other in this process; each workload's buffers are freed
+    before the next is built."""
+    import torch
+    out = {}
+    for key, name, warmup, steps, target in CONFIG_SUITE:
+        wl = make_workload(name)
+        torch.cuda.synchronize()
+        ms = timed_steps(wl, warmup, steps, hold_cycles)
+        gbs = wl.step_bytes / (ms * 1e-3) / 1e9
+        us = ms * 1e3
+        t70 = wl.step_bytes / (0.7 * PEAK_HBM_GBS * 1e9) * 1e6
+        out[key] = {"workload": WORKLOADS[name], "us_per_step": round(us, 3),
+                    "gbs": round(gbs, 1), "pct_of_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
+                    "bytes_per_step": wl.step_bytes, "steps": steps, "warmup": warmup,
+                    "us_at_70pct": round(t70, 2),
+                    "baseline_md_target_us": target,
+                    "meets_target": (us <= target) if target is not None else None}
+        del wl
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return out
 
 
 def main():
@@ -205,6 +329,8 @@ def main():
                          "while the host queues the first steps (0: no hold)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="headline only: skip the per-config block (configs)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -223,30 +349,12 @@ def main():
 
     if args.workload == "refshapes":
         return refshapes(wl, args)
-
-    for k in range(args.warmup):
-        wl.step(k)
-    torch.cuda.synchronize()
+    if args.workload == "floor":
+        return floor(args)
 
     # Timed region: exactly K steps between two events on the launch stream.
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     hold_cycles = hold_cycles_for(args.hold_us) if args.hold_us > 0 else 0
-    torch.cuda.synchronize()
-    if hold_cycles:
-        # A bounded spin kernel holds the stream while the host queues the
-        # first steps, so the start event is followed by work that is already
-        # queued (the "blocking kernel" of GPU benchmark harnesses).  Without
-        # it the GPU idles after the start event until the host's first
-        # launches arrive, about 10 us, which at K = 20 steps reads as
-        # ~0.6 us per step of host latency.  The spin runs before the start
-        # event, outside the timed region.
-        torch.cuda._sleep(hold_cycles)
-    start.record()
-    for k in range(args.steps):
-        wl.step(k)
-    stop.record()
-    torch.cuda.synchronize()
-    ms_per_step = start.elapsed_time(stop) / args.steps
+    ms_per_step = timed_steps(wl, args.warmup, args.steps, hold_cycles)
     step_bytes = wl.step_bytes
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
@@ -308,8 +416,13 @@ def main():
             "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
             "algorithmic_bytes": wl.bytes[dom], "avg_us": round(op_ms[dom] * 1e3, 3)}
-        line["cpu_baseline"] = None if args.no_cpu else cpu_baseline(wl.host_inputs(0),
-                                                                      args.cpu_seconds)
+        host_in = None if args.no_cpu else wl.host_inputs(0)
+        if not args.no_configs:
+            del wl
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+            line["configs"] = config_suite(hold_cycles)
+        line["cpu_baseline"] = None if args.no_cpu else cpu_baseline(host_in, args.cpu_seconds)
     print(json.dumps(line), flush=True)
 
 

@@ -1,0 +1,246 @@
+// Floors that a LayerNorm / bias+GELU step cannot beat on this GPU, measured
+// with plain kernels in the step's own launch structure, beside the library's
+// own steps in the same process (bench.py --workload floor).
+//
+//   empty_chain   K dependent launches of an empty kernel of G workgroups
+//                 (256 threads) per step, K = 1, 2, 3, G = 48, 256, 2048,
+//                 16384: the fixed cost of a dependent launch;
+//   config0_floor BASELINE config 0's bytes in its three dependent launches,
+//                 as plain streaming kernels: a copy of [4096, 768] (the
+//                 LayerNorm forward's 25.2 MB), an a + b -> c of [4096, 768]
+//                 (the backward's 37.7 MB) and an empty 48-workgroup launch
+//                 (the dgamma/dbeta finalize);
+//   config0_step  the library's config-0 step (layernorm_forward_save +
+//                 layernorm_backward through include/kernels.h);
+//   headline_floor the headline step's bytes in its six launches, in its
+//                 order: copy [8192, 768], copy [8192, 3072], a + b -> c
+//                 [8192, 768], empty 48, a + b -> c [8192, 3072], empty 96;
+//   headline_step the library's headline step (LayerNorm forward + backward
+//                 on [8192, 768], bias+GELU forward + backward on
+//                 [8192, 3072]).
+//
+// Every case rotates buffer sets so that at least 1 GB of other data passes
+// between two uses of a tensor (more than the 256 MB last-level cache), as
+// bench.py does; the streaming kernels use 16-byte non-temporal accesses in a
+// 16384 x 256 grid-stride loop (the fastest plain copy form measured here).
+// Times are HIP events around `iters` steps after 20 warm-up steps, on the
+// per-thread default stream.  Prints one JSON object.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <functional>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "kernels.h"
+
+namespace {
+
+#define CK(x)                                                                     \
+    do {                                                                          \
+        hipError_t e_ = (x);                                                      \
+        if (e_ != hipSuccess) {                                                   \
+            std::fprintf(stderr, "HIP error at %s:%d: %s\n", __FILE__, __LINE__,  \
+                         hipGetErrorString(e_));                                  \
+            std::exit(EXIT_FAILURE);                                              \
+        }                                                                         \
+    } while (0)
+
+constexpr int kThreads = 256;
+constexpr int kStreamBlocks = 16384;
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(kThreads) void empty_kernel() {}
+
+__global__ __launch_bounds__(kThreads) void copy_kernel(const f4* __restrict__ a,
+                                                        f4* __restrict__ c, long long n) {
+    const long long step = static_cast<long long>(gridDim.x) * kThreads;
+    for (long long i = blockIdx.x * kThreads + threadIdx.x; i < n; i += step)
+        __builtin_nontemporal_store(__builtin_nontemporal_load(a + i), c + i);
+}
+
+__global__ __launch_bounds__(kThreads) void add_kernel(const f4* __restrict__ a,
+                                                       const f4* __restrict__ b,
+                                                       f4* __restrict__ c, long long n) {
+    const long long step = static_cast<long long>(gridDim.x) * kThreads;
+    for (long long i = blockIdx.x * kThreads + threadIdx.x; i < n; i += step)
+        __builtin_nontemporal_store(__builtin_nontemporal_load(a + i) +
+                                        __builtin_nontemporal_load(b + i),
+                                    c + i);
+}
+
+hipStream_t st() { return hipStreamPerThread; }
+
+void empty(int blocks) {
+    hipLaunchKernelGGL(empty_kernel, dim3(blocks), dim3(kThreads), 0, st());
+}
+
+void copy(const float* a, float* c, long long n) {
+    hipLaunchKernelGGL(copy_kernel, dim3(kStreamBlocks), dim3(kThreads), 0, st(),
+                       reinterpret_cast<const f4*>(a), reinterpret_cast<f4*>(c), n / 4);
+}
+
+void add(const float* a, const float* b, float* c, long long n) {
+    hipLaunchKernelGGL(add_kernel, dim3(kStreamBlocks), dim3(kThreads), 0, st(),
+                       reinterpret_cast<const f4*>(a), reinterpret_cast<const f4*>(b),
+                       reinterpret_cast<f4*>(c), n / 4);
+}
+
+float* buf(size_t n, float v) {
+    float* p = nullptr;
+    CK(hipMalloc(&p, n * sizeof(float)));
+    std::vector<float> h(n, v);
+    CK(hipMemcpy(p, h.data(), n * sizeof(float), hipMemcpyHostToDevice));
+    return p;
+}
+
+// Microseconds per step over `iters` steps after 20 warm-up steps.
+double time_steps(const std::function<void(int)>& step, int iters) {
+    for (int k = 0; k < 20; ++k) step(k);
+    CK(hipDeviceSynchronize());
+    hipEvent_t a, b;
+    CK(hipEventCreate(&a));
+    CK(hipEventCreate(&b));
+    CK(hipEventRecord(a, st()));
+    for (int k = 0; k < iters; ++k) step(20 + k);
+    CK(hipEventRecord(b, st()));
+    CK(hipEventSynchronize(b));
+    float ms = 0.0f;
+    CK(hipEventElapsedTime(&ms, a, b));
+    CK(hipGetLastError());
+    CK(hipEventDestroy(a));
+    CK(hipEventDestroy(b));
+    return 1e3 * ms / iters;
+}
+
+// One buffer set of a LayerNorm (+ optional bias+GELU) step: inputs of the
+// forward and the backward, outputs, statistics.
+struct Set {
+    float *x, *y, *mean, *rstd, *dy, *dx;  // LayerNorm [R, C]
+    float *h, *o, *dh, *gin;               // bias+GELU [R, F] (F = 0: none)
+};
+
+std::vector<Set> make_sets(int n, int R, int C, int F, const float* gamma, const float* beta) {
+    std::vector<Set> s(n);
+    for (Set& e : s) {
+        const size_t rc = size_t(R) * C, rf = size_t(R) * F;
+        e.x = buf(rc, 0.5f);
+        e.y = buf(rc, 0.0f);
+        e.dy = buf(rc, 0.25f);
+        e.dx = buf(rc, 0.0f);
+        e.mean = buf(R, 0.0f);
+        e.rstd = buf(R, 0.0f);
+        e.h = F ? buf(rf, 0.1f) : nullptr;
+        e.o = F ? buf(rf, 0.0f) : nullptr;
+        e.dh = F ? buf(rf, 0.3f) : nullptr;
+        e.gin = F ? buf(rf, 0.0f) : nullptr;
+        layernorm_forward_save(e.x, gamma, beta, e.y, e.mean, e.rstd, R, C);
+    }
+    CK(hipDeviceSynchronize());
+    return s;
+}
+
+void free_sets(std::vector<Set>& s) {
+    CK(hipDeviceSynchronize());
+    for (Set& e : s)
+        for (float* p : {e.x, e.y, e.dy, e.dx, e.mean, e.rstd, e.h, e.o, e.dh, e.gin})
+            if (p) CK(hipFree(p));
+    s.clear();
+}
+
+int sets_for(size_t set_bytes) {
+    const size_t want = (size_t(1) << 30) / set_bytes + 2;
+    return static_cast<int>(want < 4 ? 4 : (want > 64 ? 64 : want));
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    const int scale = argc > 1 ? std::atoi(argv[1]) : 1;
+    std::vector<std::pair<std::string, double>> out;
+
+    for (int blocks : {48, 256, 2048, 16384})
+        for (int k = 1; k <= 3; ++k)
+            out.emplace_back("empty_chain_" + std::to_string(k) + "x" + std::to_string(blocks),
+                             time_steps([&](int) {
+                                 for (int j = 0; j < k; ++j) empty(blocks);
+                             }, 2000 * scale));
+
+    const int C = 768;
+    float* gamma = buf(4096, 1.0f);
+    float* beta = buf(4096, 0.0f);
+
+    // Config 0: [4096, 768].
+    {
+        const int R = 4096;
+        const long long n = 1ll * R * C;
+        std::vector<Set> s = make_sets(sets_for(6 * n * 4), R, C, 0, gamma, beta);
+        const int ns = static_cast<int>(s.size());
+        float* dg = buf(C, 0.0f);
+        float* db = buf(C, 0.0f);
+        out.emplace_back("config0_floor", time_steps([&](int k) {
+                             const Set& f = s[k % ns];
+                             const Set& b = s[(k + ns - 1) % ns];
+                             copy(f.x, f.y, n);
+                             add(b.dy, b.x, b.dx, n);
+                             empty(48);
+                         }, 400 * scale));
+        out.emplace_back("config0_step", time_steps([&](int k) {
+                             const Set& f = s[k % ns];
+                             const Set& b = s[(k + ns - 1) % ns];
+                             layernorm_forward_save(f.x, gamma, beta, f.y, f.mean, f.rstd, R, C);
+                             layernorm_backward(b.dy, b.x, b.mean, b.rstd, gamma, b.dx, dg, db, R,
+                                                C);
+                         }, 400 * scale));
+        free_sets(s);
+        CK(hipFree(dg));
+        CK(hipFree(db));
+    }
+
+    // Headline: [8192, 768] and [8192, 3072].
+    {
+        const int R = 8192, F = 3072;
+        const long long n = 1ll * R * C, nf = 1ll * R * F;
+        float* bias = buf(F, 0.01f);
+        std::vector<Set> s = make_sets(sets_for((6 * n + 4 * nf) * 4), R, C, F, gamma, beta);
+        const int ns = static_cast<int>(s.size());
+        float* dg = buf(C, 0.0f);
+        float* db = buf(C, 0.0f);
+        float* dbias = buf(F, 0.0f);
+        out.emplace_back("headline_floor", time_steps([&](int k) {
+                             const Set& f = s[k % ns];
+                             const Set& b = s[(k + ns - 1) % ns];
+                             copy(f.x, f.y, n);
+                             copy(f.h, f.o, nf);
+                             add(b.dy, b.x, b.dx, n);
+                             empty(48);
+                             add(b.h, b.dh, b.gin, nf);
+                             empty(96);
+                         }, 200 * scale));
+        out.emplace_back("headline_step", time_steps([&](int k) {
+                             const Set& f = s[k % ns];
+                             const Set& b = s[(k + ns - 1) % ns];
+                             layernorm_forward_save(f.x, gamma, beta, f.y, f.mean, f.rstd, R, C);
+                             bias_gelu_forward(f.h, bias, f.o, R, F);
+                             layernorm_backward(b.dy, b.x, b.mean, b.rstd, gamma, b.dx, dg, db, R,
+                                                C);
+                             gelu_backward_with_bias_backward(b.h, bias, b.dh, b.gin, dbias, R,
+                                                              F);
+                         }, 200 * scale));
+        free_sets(s);
+        CK(hipFree(dg));
+        CK(hipFree(db));
+        CK(hipFree(dbias));
+        CK(hipFree(bias));
+    }
+    CK(hipFree(gamma));
+    CK(hipFree(beta));
+
+    std::printf("{");
+    for (size_t i = 0; i < out.size(); ++i)
+        std::printf("%s\"%s\": %.4f", i ? ", " : "", out[i].first.c_str(), out[i].second);
+    std::printf("}\n");
+    return 0;
+}

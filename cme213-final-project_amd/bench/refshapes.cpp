@@ -1,13 +1,21 @@
-// The reference's own fused-versus-unfused timing loops, at its shapes,
-// through the drop-in C++ interface (include/kernels.h):
-//   FINAL_CLEAN_CODE/tests/test_fusion_benchmark.cu (bias+ReLU 2048x512,
-//   residual+LayerNorm forward and LayerNorm backward + residual 2048x128:
-//   10 warm-up calls, then `iters` calls on the same buffers between two
-//   events) and the LayerNorm forward of correctness_matrix (2048x128).
-// Inputs use the reference harness's sin/cos fill pattern.  Calls launch on
-// the per-thread default stream, as the reference's do; the events are
-// recorded there.  Prints one JSON object: microseconds per call per case.
-// Run by bench.py --workload refshapes.
+// The reference's own kernel timing loops, at its shapes, through the
+// drop-in C++ interface (include/kernels.h):
+//   * FINAL_CLEAN_CODE/tests/test_fusion_benchmark.cu: bias+ReLU 2048x512,
+//     residual+LayerNorm forward and LayerNorm backward + residual 2048x128,
+//     fused and unfused (10 warm-up calls, then `iters` calls on the same
+//     buffers between two events), and the LayerNorm forward of
+//     correctness_matrix (2048x128); inputs: the fusion harness's sin/cos
+//     fill pattern;
+//   * FINAL_CLEAN_CODE/tests/benchmark_all.cu:124-163, the LayerNorm
+//     bandwidth grid (six shapes, 10 warm-up calls, 200 timed);
+//   * FINAL_CLEAN_CODE/tests/deep_profile.cu:121-173, LayerNorm forward at
+//     2048x{128,256,512} (20 warm-up calls, 500 timed);
+//   the last two with their srand(42), rand()/RAND_MAX - 0.5 inputs,
+//   gamma = 1, beta = 0.
+// Calls launch on the per-thread default stream, as the reference's do; the
+// events are recorded there.  Prints one JSON object: per case, microseconds
+// per call and the number of timed calls.  Run by bench.py --workload
+// refshapes.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -54,9 +62,22 @@ float* dev_zero(int n) {
     return p;
 }
 
-double time_us(const std::function<void()>& call, int iters) {
+// The reference harnesses' input generator (glibc rand() after srand(seed)).
+std::vector<float> rand_unit(int n, unsigned seed = 42) {
+    std::vector<float> v(n);
+    std::srand(seed);
+    for (auto& x : v) x = static_cast<float>(std::rand()) / static_cast<float>(RAND_MAX) - 0.5f;
+    return v;
+}
+
+struct Timed {
+    double us;
+    int calls;
+};
+
+Timed time_us(const std::function<void()>& call, int iters, int warmup = 10) {
     hipStream_t st = hipStreamPerThread;
-    for (int i = 0; i < 10; ++i) call();
+    for (int i = 0; i < warmup; ++i) call();
     CK(hipDeviceSynchronize());
     hipEvent_t a, b;
     CK(hipEventCreate(&a));
@@ -69,7 +90,7 @@ double time_us(const std::function<void()>& call, int iters) {
     CK(hipEventElapsedTime(&ms, a, b));
     CK(hipEventDestroy(a));
     CK(hipEventDestroy(b));
-    return 1e3 * ms / iters;
+    return {1e3 * ms / iters, iters};
 }
 
 }  // namespace
@@ -99,7 +120,7 @@ int main(int argc, char** argv) {
     float* bout = dev_zero(nb);
     CK(hipDeviceSynchronize());
 
-    std::vector<std::pair<std::string, double>> r;
+    std::vector<std::pair<std::string, Timed>> r;
     r.emplace_back("ln_fwd", time_us([&] { layernorm_forward(x, gamma, beta, out, R, C); },
                                      300 * scale));
     r.emplace_back("residual_ln_unfused", time_us([&] {
@@ -124,9 +145,39 @@ int main(int argc, char** argv) {
     r.emplace_back("bias_relu_fused",
                    time_us([&] { bias_relu_forward(work, bias, bout, Rb, Cb); }, 200 * scale));
 
+    // LayerNorm forward grids of benchmark_all.cu (10 + 200 calls) and
+    // deep_profile.cu (20 + 500 calls), gamma = 1, beta = 0.
+    struct Grid {
+        const char* tag;
+        int rows, cols, warmup, iters;
+    };
+    const Grid grids[] = {{"ln_grid", 1024, 64, 10, 200},   {"ln_grid", 1024, 128, 10, 200},
+                          {"ln_grid", 2048, 128, 10, 200},  {"ln_grid", 4096, 128, 10, 200},
+                          {"ln_grid", 2048, 256, 10, 200},  {"ln_grid", 2048, 512, 10, 200},
+                          {"ln_deep", 2048, 128, 20, 500},  {"ln_deep", 2048, 256, 20, 500},
+                          {"ln_deep", 2048, 512, 20, 500}};
+    for (const Grid& gd : grids) {
+        const int gn = gd.rows * gd.cols;
+        float* gx = dev(rand_unit(gn));
+        float* gg = dev(std::vector<float>(gd.cols, 1.0f));
+        float* gb = dev(std::vector<float>(gd.cols, 0.0f));
+        float* gy = dev_zero(gn);
+        CK(hipDeviceSynchronize());
+        const std::string name = std::string(gd.tag) + "_" + std::to_string(gd.rows) + "x" +
+                                 std::to_string(gd.cols);
+        r.emplace_back(name, time_us([&] { layernorm_forward(gx, gg, gb, gy, gd.rows, gd.cols); },
+                                     gd.iters * scale, gd.warmup));
+        CK(hipDeviceSynchronize());
+        CK(hipFree(gx));
+        CK(hipFree(gg));
+        CK(hipFree(gb));
+        CK(hipFree(gy));
+    }
+
     std::printf("{");
     for (size_t i = 0; i < r.size(); ++i)
-        std::printf("%s\"%s\": %.4f", i ? ", " : "", r[i].first.c_str(), r[i].second);
+        std::printf("%s\"%s\": {\"us\": %.4f, \"calls\": %d}", i ? ", " : "",
+                    r[i].first.c_str(), r[i].second.us, r[i].second.calls);
     std::printf("}\n");
     return 0;
 }

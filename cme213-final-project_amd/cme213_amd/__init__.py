@@ -178,11 +178,30 @@ def _i(x):
     return _ptr(x, torch.int32)
 
 
+def _resolve_current_stream():
+    """Returns a function that gives the raw hipStream_t of torch's current
+    stream on the current device.  torch's private binding
+    (_cuda_getCurrentRawStream) costs about a microsecond per call; if a torch
+    release renames it, the public torch.cuda.current_stream().cuda_stream
+    (a few microseconds) is used instead.  Resolved once, at import."""
+    try:
+        import torch
+    except ImportError:
+        return lambda: None
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    dev = getattr(torch._C, "_cuda_getDevice", None)
+    if raw is not None and dev is not None:
+        return lambda: raw(dev())
+    return lambda: torch.cuda.current_stream().cuda_stream
+
+
+_current_stream = _resolve_current_stream()
+
+
 def _stream(stream):
     if stream is not None:
         return stream
-    import torch
-    return torch._C._cuda_getCurrentRawStream(torch._C._cuda_getDevice())
+    return _current_stream()
 
 
 class Bound:
@@ -213,8 +232,7 @@ class Bound:
     def __call__(self):
         st = self._stream
         if st is None:
-            import torch
-            st = torch._C._cuda_getCurrentRawStream(torch._C._cuda_getDevice())
+            st = _current_stream()
         rc = self._fn(*self._args, st)
         if rc != MI_OK:
             raise MIError(rc, last_error())

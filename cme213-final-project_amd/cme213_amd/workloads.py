@@ -201,12 +201,22 @@ class BlockSequence:
 
     def step(self, k):
         """One training step's non-GEMM work: forward over all layers, then
-        backward over all layers (a fixed upstream gradient), issued as
-        bound C-ABI calls."""
+        backward over all layers, issued as bound C-ABI calls.
+
+        The residual-stream gradient buffer is set to a synthetic upstream
+        gradient once, before the first step; every step's backward then
+        accumulates its 2 L LayerNorm-backward terms onto the value it finds
+        (`+=`, as the reference's layernorm_backward_residual does).  In the
+        reference that buffer is written by the output-projection GEMM at the
+        start of each backward (FINAL_CLEAN_CODE/src/model/transformer.cu:459,
+        gemm_tiled_BT into act.grad_residual2), which is outside this path,
+        so no stand-in for it runs inside the step: the kernels, their
+        arguments and the bytes they move are the same every step."""
         if not hasattr(self, "_calls"):
             g = torch.Generator(device="cuda")
             g.manual_seed(11)
             self.gtop = _randn((self.R, self.C), g)
+            self.gres.copy_(self.gtop)
             self._calls = self._bind_step()
         for fn in self._calls:
             fn()
@@ -223,8 +233,6 @@ class BlockSequence:
                               p["b2"], a["r2"], a["y2"], a["m2"], a["s2"], R, C, 1e-5))
             calls.append(bind("mi_bias_gelu_forward", i["h"], p["bias"], a["o"], R, F))
             r = a["r2"]
-        # the residual-stream gradient starts from the upstream gradient
-        calls.append(lambda: self.gres.copy_(self.gtop))
         for l in reversed(range(self.L)):
             i, p, a, gr = self._in(l), self.params[l], self.act[l], self.grads[l]
             calls.append(bind("mi_gelu_backward_with_bias_backward", i["h"], p["bias"], i["gh"],
@@ -418,24 +426,33 @@ class Relu16:
 
 
 class RefShapes:
-    """The reference's own fused-versus-unfused kernel benchmarks, at its own
-    shapes and with its own loop (FINAL_CLEAN_CODE/tests/test_fusion_benchmark.cu:
-    bias+ReLU 2048x512; residual+LN forward and LN backward+residual
-    2048x128; the same call repeated on the same buffers after 10 warm-up
-    calls, so the tensors stay cache-resident, as in the reference) plus the
-    LN forward of results/correctness_matrix_85267.md:24 (2048x128).  The
-    loops run in C++ through include/kernels.h (bench/refshapes.cpp, built
-    as refshapes_bench next to the library), as the reference's do: from
-    Python the ctypes call overhead (~7 us) would exceed these kernels.
+    """The reference's own kernel benchmarks, at its own shapes and with its
+    own loops, run in C++ through include/kernels.h (bench/refshapes.cpp,
+    built as refshapes_bench next to the library), as the reference's are:
+    from Python the ctypes call overhead (~7 us) would exceed these kernels.
+    The same call repeats on the same buffers, so the tensors stay
+    cache-resident, as in the reference.
 
-    Bytes follow the reference's model (profile_fusion_kernels.cu:30-55): a
-    multiple of nbytes = rows*cols*4 per call; the LN forward uses the
-    "effective BW" 2*rows*cols*4 of correctness_matrix.  CASES also holds the
-    reference's numbers on its Quadro RTX 6000 (672 GB/s): CUDA-event time
-    per call (results/final_clean_main_table.csv:57-65;
-    correctness_matrix_85267.md:24 for the LN forward) and Nsight Compute
-    kernel time (results/roofline_fusion.csv:2-7).  Context, not a same-node
-    comparison."""
+      * fused-versus-unfused pairs of FINAL_CLEAN_CODE/tests/
+        test_fusion_benchmark.cu (bias+ReLU 2048x512; residual+LN forward and
+        LN backward+residual 2048x128) and the LN forward of
+        results/correctness_matrix_85267.md:24 (2048x128).  Bytes follow the
+        reference's model (profile_fusion_kernels.cu:30-55): a multiple of
+        nbytes = rows*cols*4 per call; the LN forward uses the "effective BW"
+        2*rows*cols*4 of correctness_matrix.  Reference figures on its Quadro
+        RTX 6000 (672 GB/s): CUDA-event time per call
+        (results/final_clean_main_table.csv:57-65; correctness_matrix_85267.md:24
+        for the LN forward) and Nsight Compute kernel time
+        (results/roofline_fusion.csv:2-7).
+      * the LayerNorm bandwidth grid of tests/benchmark_all.cu:124-163 (six
+        shapes, bytes 2*rows*cols*4 as it counts them), with its logged
+        event times (FINAL_CLEAN_CODE_/logs/full_validation_88905.out:209-214,
+        and the slower run full_validation_89398.out:214-219);
+      * the LayerNorm forward of tests/deep_profile.cu:121-173 at
+        2048x{128,256,512} (bytes (2*rows*cols + 2*cols)*4 as it counts
+        them); the reference tree holds no logged output of it.
+
+    Context, not a same-node comparison."""
 
     CASES = {
         # name: (rows, cols, bytes in units of nbytes, ref event us, ref ncu us)
@@ -447,22 +464,40 @@ class RefShapes:
         "bias_relu_unfused": (2048, 512, 5.0, 22.6, 32.90),
         "bias_relu_fused": (2048, 512, 4.0, 15.7, 14.62),
     }
+    # benchmark_all.cu's grid: (rows, cols) -> (ref event us, slower run us)
+    GRID = {(1024, 64): (3.3, 4.5), (1024, 128): (4.5, 6.1), (2048, 128): (7.0, 9.4),
+            (4096, 128): (11.6, 15.5), (2048, 256): (11.7, 15.7), (2048, 512): (21.5, 25.1)}
+    DEEP = [(2048, 128), (2048, 256), (2048, 512)]
     HARNESS = "refshapes_bench"
 
     def __init__(self):
         import os
-        self.seed = None
+        self.seed = 42
         self.bytes = {k: int(m * r * c * F32) for k, (r, c, m, _, _) in self.CASES.items()}
+        for (r, c) in self.GRID:
+            self.bytes[f"ln_grid_{r}x{c}"] = 2 * r * c * F32
+        for (r, c) in self.DEEP:
+            self.bytes[f"ln_deep_{r}x{c}"] = (2 * r * c + 2 * c) * F32
         self.step_bytes = sum(self.bytes.values())
         self.harness = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
                                     self.HARNESS)
 
+    def names(self):
+        return list(self.bytes)
+
     def published(self, name):
-        _, _, _, ev, ncu = self.CASES[name]
-        return {"event_us": ev, "ncu_us": ncu}
+        """The reference's figures for a case (None where it has none)."""
+        if name in self.CASES:
+            _, _, _, ev, ncu = self.CASES[name]
+            return {"event_us": ev, "ncu_us": ncu}
+        if name.startswith("ln_grid_"):
+            r, c = (int(v) for v in name[len("ln_grid_"):].split("x"))
+            ev, ev2 = self.GRID[(r, c)]
+            return {"event_us": ev, "event_us_other_run": ev2, "ncu_us": None}
+        return {"event_us": None, "ncu_us": None}
 
     def run(self, scale=1):
-        """Runs the C++ harness; returns {case: microseconds per call}."""
+        """Runs the C++ harness; returns {case: {"us": per call, "calls": timed calls}}."""
         import json
         import subprocess
         out = subprocess.run([self.harness, str(scale)], capture_output=True, text=True,
