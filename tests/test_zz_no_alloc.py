@@ -51,3 +51,64 @@ def test_noalloc_rejects_shapes_beyond_the_scratch(dev):
     rc = M.lib.mi_layernorm_backward_noalloc(p, p, p, p, p, p, p, p, rows, cols, None)
     assert rc == M.MI_ERR_INVALID_ARG
     assert "scratch" in M.last_error()
+
+
+def test_noalloc_uses_no_workspace_and_replays_in_a_graph(dev):
+    """The entry point's defining property: with the library workspace
+    released (0 bytes), an eager call and a graph capture of the call leave
+    it at 0 bytes (no allocation, no use of the workspace), and every replay
+    of the graph, with eager work between replays, equals the eager result
+    bit for bit."""
+    rows, cols = 4096, 768
+    x, gamma, _, g = ln_inputs(rows, cols, 950)
+    _, m, s = O.layernorm_forward(x, gamma, np.zeros(cols, np.float32))
+    G, X, Mn, Rs, Gm = dev_t(g), dev_t(x), dev_t(m), dev_t(s), dev_t(gamma)
+    DX = torch.empty(rows, cols, device=dev)
+    DG, DB = torch.empty(cols, device=dev), torch.empty(cols, device=dev)
+
+    def step():
+        DG.fill_(0.0)  # zero_grad by fill kernels inside the graph (no memset node)
+        DB.fill_(0.0)
+        M.layernorm_backward_noalloc(G, X, Mn, Rs, Gm, DX, DG, DB, rows, cols)
+
+    M.workspace_release()
+    assert M.workspace_bytes() == 0
+    note("layernorm_backward_noalloc eager, workspace released")
+    step()
+    torch.cuda.synchronize()
+    assert M.workspace_bytes() == 0
+    ref = [host(t) for t in (DX, DG, DB)]
+    want = _run(M.layernorm_backward, g, x, m, s, gamma, np.zeros(cols, np.float32),
+                np.zeros(cols, np.float32), rows, cols)
+    for name, a, b in zip(("dx", "dgamma", "dbeta"), ref, want):
+        assert_exact(f"noalloc eager {name}", a, b)
+    # the workspace entry point just grew the workspace; release it again
+    M.workspace_release()
+    assert M.workspace_bytes() == 0
+
+    note("layernorm_backward_noalloc under graph capture, no workspace reserved")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+    assert M.workspace_bytes() == 0
+    for rep in range(3):
+        for t in (DX, DG, DB):
+            t.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, t, r in zip(("dx", "dgamma", "dbeta"), (DX, DG, DB), ref):
+            assert_exact(f"replay {rep} {name}", host(t), r)
+        step()  # eager work between replays
+        torch.cuda.synchronize()
+        for name, t, r in zip(("dx", "dgamma", "dbeta"), (DX, DG, DB), ref):
+            assert_exact(f"eager after replay {rep} {name}", host(t), r)
+    assert M.workspace_bytes() == 0
+    del graph
+    torch.cuda.synchronize()
