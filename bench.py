@@ -251,10 +251,12 @@ def floor(args):
         "dependent_launch_us_by_workgroups": per_launch,
         "config0": {"bytes": c0, "floor_us": round(t["config0_floor"], 3),
                     "step_us": round(t["config0_step"], 3),
+                    "step_host_issue_us": round(t["config0_step_host"], 3),
                     "step_minus_floor_us": round(t["config0_step"] - t["config0_floor"], 3),
                     "us_at_70pct": round(c0 / (0.7 * PEAK_HBM_GBS * 1e9) * 1e6, 2)},
         "headline": {"bytes": hb, "floor_us": round(t["headline_floor"], 3),
                      "step_us": round(t["headline_step"], 3),
+                     "step_host_issue_us": round(t["headline_step_host"], 3),
                      "floor_pct_of_peak": round(100 * hb / (t["headline_floor"] * 1e-6) / 1e9 /
                                                 PEAK_HBM_GBS, 2),
                      "step_pct_of_peak": round(100 * hb / (t["headline_step"] * 1e-6) / 1e9 /

@@ -18,6 +18,9 @@
 //   headline_step the library's headline step (LayerNorm forward + backward
 //                 on [8192, 768], bias+GELU forward + backward on
 //                 [8192, 3072]).
+// Each *_floor / *_step case also reports *_host: the host's time to issue
+// one step (the launches only), against which the GPU time shows whether a
+// step is bound by the host's launch rate.
 //
 // Every case rotates buffer sets so that at least 1 GB of other data passes
 // between two uses of a tensor (more than the 256 MB last-level cache), as
@@ -27,6 +30,7 @@
 // per-thread default stream.  Prints one JSON object.
 #include <hip/hip_runtime.h>
 
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <functional>
@@ -96,7 +100,13 @@ float* buf(size_t n, float v) {
     return p;
 }
 
-// Microseconds per step over `iters` steps after 20 warm-up steps.
+// Host time to issue one step, microseconds (set by time_steps).
+double g_host_us = 0.0;
+
+// Microseconds per step over `iters` steps after 20 warm-up steps (GPU time
+// between two events); g_host_us receives the host's issue time per step
+// over the same loop.  A step whose host time reaches its GPU time is bound
+// by the host's launch rate, not by the GPU.
 double time_steps(const std::function<void(int)>& step, int iters) {
     for (int k = 0; k < 20; ++k) step(k);
     CK(hipDeviceSynchronize());
@@ -104,7 +114,9 @@ double time_steps(const std::function<void(int)>& step, int iters) {
     CK(hipEventCreate(&a));
     CK(hipEventCreate(&b));
     CK(hipEventRecord(a, st()));
+    const auto t0 = std::chrono::steady_clock::now();
     for (int k = 0; k < iters; ++k) step(20 + k);
+    const auto t1 = std::chrono::steady_clock::now();
     CK(hipEventRecord(b, st()));
     CK(hipEventSynchronize(b));
     float ms = 0.0f;
@@ -112,6 +124,7 @@ double time_steps(const std::function<void(int)>& step, int iters) {
     CK(hipGetLastError());
     CK(hipEventDestroy(a));
     CK(hipEventDestroy(b));
+    g_host_us = std::chrono::duration<double, std::micro>(t1 - t0).count() / iters;
     return 1e3 * ms / iters;
 }
 
@@ -160,6 +173,11 @@ int sets_for(size_t set_bytes) {
 int main(int argc, char** argv) {
     const int scale = argc > 1 ? std::atoi(argv[1]) : 1;
     std::vector<std::pair<std::string, double>> out;
+    // time a case and record its GPU and host-issue times per step
+    auto rec = [&](const std::string& name, const std::function<void(int)>& step, int iters) {
+        out.emplace_back(name, time_steps(step, iters));
+        out.emplace_back(name + "_host", g_host_us);
+    };
 
     for (int blocks : {48, 256, 2048, 16384})
         for (int k = 1; k <= 3; ++k)
@@ -180,20 +198,20 @@ int main(int argc, char** argv) {
         const int ns = static_cast<int>(s.size());
         float* dg = buf(C, 0.0f);
         float* db = buf(C, 0.0f);
-        out.emplace_back("config0_floor", time_steps([&](int k) {
+        rec("config0_floor", [&](int k) {
                              const Set& f = s[k % ns];
                              const Set& b = s[(k + ns - 1) % ns];
                              copy(f.x, f.y, n);
                              add(b.dy, b.x, b.dx, n);
                              empty(48);
-                         }, 400 * scale));
-        out.emplace_back("config0_step", time_steps([&](int k) {
+                         }, 400 * scale);
+        rec("config0_step", [&](int k) {
                              const Set& f = s[k % ns];
                              const Set& b = s[(k + ns - 1) % ns];
                              layernorm_forward_save(f.x, gamma, beta, f.y, f.mean, f.rstd, R, C);
                              layernorm_backward(b.dy, b.x, b.mean, b.rstd, gamma, b.dx, dg, db, R,
                                                 C);
-                         }, 400 * scale));
+                         }, 400 * scale);
         free_sets(s);
         CK(hipFree(dg));
         CK(hipFree(db));
@@ -209,7 +227,7 @@ int main(int argc, char** argv) {
         float* dg = buf(C, 0.0f);
         float* db = buf(C, 0.0f);
         float* dbias = buf(F, 0.0f);
-        out.emplace_back("headline_floor", time_steps([&](int k) {
+        rec("headline_floor", [&](int k) {
                              const Set& f = s[k % ns];
                              const Set& b = s[(k + ns - 1) % ns];
                              copy(f.x, f.y, n);
@@ -218,8 +236,8 @@ int main(int argc, char** argv) {
                              empty(48);
                              add(b.h, b.dh, b.gin, nf);
                              empty(96);
-                         }, 200 * scale));
-        out.emplace_back("headline_step", time_steps([&](int k) {
+                         }, 200 * scale);
+        rec("headline_step", [&](int k) {
                              const Set& f = s[k % ns];
                              const Set& b = s[(k + ns - 1) % ns];
                              layernorm_forward_save(f.x, gamma, beta, f.y, f.mean, f.rstd, R, C);
@@ -228,7 +246,7 @@ int main(int argc, char** argv) {
                                                 C);
                              gelu_backward_with_bias_backward(b.h, bias, b.dh, b.gin, dbias, R,
                                                               F);
-                         }, 200 * scale));
+                         }, 200 * scale);
         free_sets(s);
         CK(hipFree(dg));
         CK(hipFree(db));
