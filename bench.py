@@ -22,11 +22,12 @@ Also reported on the same line:
                 its OpenMP row loops on OMP_NUM_THREADS (else all) host cores;
   breakdown_us  average duration of each operation (HIP events);
   configs       every other BASELINE config (0: ln, 1: gelu, 2: embedding,
-                3: block12, 4: xl48 and wide), each timed in the same process
-                after the headline's timed region, with its own rotating
-                buffers, warm-up and step count: time per step, GB/s, % of
-                peak and the time at 70% of peak (BASELINE.md section 2's
-                target where it states one); --no-configs skips it.
+                3: block12, 4: xl48 and wide), each timed after the headline
+                by its own `bench.py --workload NAME` command in a child
+                process (its own rotating buffers, warm-up and step count):
+                time per step, GB/s, % of peak and the time at 70% of peak
+                (BASELINE.md section 2's target where it states one);
+                --no-configs skips it.
 
 Before the timed region a bounded spin kernel (torch.cuda._sleep, about
 --hold-us) holds the stream while the host queues the first steps, so the
@@ -289,29 +290,35 @@ def timed_steps(wl, warmup, steps, hold_cycles):
     return start.elapsed_time(stop) / steps
 
 
-def config_suite(hold_cycles):
-    """Each BASELINE config's workload, timed like the headline (its own
-    rotating buffers, warm-up, spin hold and event-bracketed steps), one
-    after the other in this process; each workload's buffers are freed
-    before the next is built."""
-    import torch
+def config_suite(hold_us):
+    """Each BASELINE config's workload, timed by its own `bench.py --workload
+    NAME` command (its rotating buffers, warm-up, spin hold and
+    event-bracketed steps) in a child process, one after the other.  A fresh
+    process per config measures each as its standalone command does: run in
+    this process after the other workloads had been allocated and freed, the
+    large-footprint ones read about 1% slower (block x12 1985-1988 against
+    1966-1974 us, block x48 8473-8479 against 8380-8387 us; the embedding's
+    random table rows about 1 us slower), in either order of the configs."""
+    import subprocess
     out = {}
     for key, name, warmup, steps, target in CONFIG_SUITE:
-        wl = make_workload(name)
-        torch.cuda.synchronize()
-        ms = timed_steps(wl, warmup, steps, hold_cycles)
-        gbs = wl.step_bytes / (ms * 1e-3) / 1e9
-        us = ms * 1e3
-        t70 = wl.step_bytes / (0.7 * PEAK_HBM_GBS * 1e9) * 1e6
+        cmd = [sys.executable, os.path.join(ROOT, "bench.py"), "--workload", name, "--steps",
+               str(steps), "--warmup", str(warmup), "--no-cpu", "--hold-us", str(hold_us)]
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+        if r.returncode != 0:
+            raise SystemExit(f"bench.py: config {name} failed ({r.returncode}):\n{r.stderr[-2000:]}")
+        d = json.loads(r.stdout.strip().splitlines()[-1])
+        us = d["ms_per_step"] * 1e3
+        step_bytes = d["config"]["bytes_per_step"]
+        gbs = step_bytes / (us * 1e-6) / 1e9
+        t70 = step_bytes / (0.7 * PEAK_HBM_GBS * 1e9) * 1e6
         out[key] = {"workload": WORKLOADS[name], "us_per_step": round(us, 3),
                     "gbs": round(gbs, 1), "pct_of_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
-                    "bytes_per_step": wl.step_bytes, "steps": steps, "warmup": warmup,
+                    "bytes_per_step": step_bytes, "steps": steps, "warmup": warmup,
                     "us_at_70pct": round(t70, 2),
                     "baseline_md_target_us": target,
-                    "meets_target": (us <= target) if target is not None else None}
-        del wl
-        torch.cuda.synchronize()
-        torch.cuda.empty_cache()
+                    "meets_target": (us <= target) if target is not None else None,
+                    "command": " ".join(["python3", "bench.py"] + cmd[3:])}
     return out
 
 
@@ -423,7 +430,7 @@ def main():
             del wl
             torch.cuda.synchronize()
             torch.cuda.empty_cache()
-            line["configs"] = config_suite(hold_cycles)
+            line["configs"] = config_suite(args.hold_us)
         line["cpu_baseline"] = None if args.no_cpu else cpu_baseline(host_in, args.cpu_seconds)
     print(json.dumps(line), flush=True)
 
