@@ -134,9 +134,9 @@ WORKLOADS = {
     "ce": "softmax cross-entropy of the model loss: logits [8192,50257] (B=8, T=1024, GPT-2 vocab)",
     "adam": "optimizer step (grad norm^2 + clip + Adam) over GPT-2 small's 124,439,808 parameters",
     "relu16": "fp16 activation storage: bias+ReLU to half fwd + half-mask ReLU bwd+dbias [8192,3072]",
-    "floor": "launch and streaming floors: empty-kernel chains; config 0's and the headline's "
-             "bytes as plain streaming kernels in their own launch structure, beside the "
-             "library's steps (C++ harness)",
+    "floor": "launch and streaming floors: empty-kernel chains; config 0's, the headline's "
+             "and config 3's bytes as plain streaming kernels in their own launch structure, "
+             "beside the library's steps (C++ harness)",
     "refshapes": "the reference's kernel benchmarks at its shapes: fused/unfused LN fwd, residual+LN, "
                  "LN bwd+residual [2048,128], bias+ReLU [2048,512]; the LN forward grids of "
                  "benchmark_all.cu and deep_profile.cu (cache-resident, as the reference)",
@@ -230,8 +230,8 @@ def refshapes(wl, args):
 def floor(args):
     """The launch and streaming floors of bench/launch_floor.cpp (one JSON
     line): the cost of a dependent launch from chains of 1-3 empty kernels,
-    and the config-0 and headline steps beside the same bytes moved by plain
-    streaming kernels in the same launch structure."""
+    and the config-0, headline and config-3 (block x12) steps beside the same
+    bytes moved by plain streaming kernels in the same launch structure."""
     import subprocess
     exe = os.path.join(ROOT, "cme213-final-project_amd", "launch_floor")
     out = subprocess.run([exe, str(max(1, args.steps // 200))], capture_output=True, text=True,
@@ -239,9 +239,13 @@ def floor(args):
     t = json.loads(out.strip().splitlines()[-1])
     per_launch = {str(g): round((t[f"empty_chain_3x{g}"] - t[f"empty_chain_1x{g}"]) / 2, 3)
                   for g in (48, 256, 2048, 16384)}
-    from cme213_amd.workloads import headline_bytes, ln_bwd_bytes, ln_fwd_bytes
+    from cme213_amd.workloads import (gelu_bwd_bytes, gelu_fwd_bytes, headline_bytes,
+                                      ln_bwd_bytes, ln_bwd_residual_bytes, ln_fwd_bytes,
+                                      res_ln_fwd_bytes)
     c0 = ln_fwd_bytes(4096, 768) + ln_bwd_bytes(4096, 768)
     hb = sum(headline_bytes().values())
+    b12 = 12 * (2 * res_ln_fwd_bytes(8192, 768) + gelu_fwd_bytes(8192, 3072)
+                + gelu_bwd_bytes(8192, 3072) + 2 * ln_bwd_residual_bytes(8192, 768))
     print(json.dumps({
         "metric": "config-0 step time against its plain-kernel floor", "value":
             round(t["config0_step"], 3), "unit": "us", "n_gpus": 1, "steps": None,
@@ -261,7 +265,15 @@ def floor(args):
                      "floor_pct_of_peak": round(100 * hb / (t["headline_floor"] * 1e-6) / 1e9 /
                                                 PEAK_HBM_GBS, 2),
                      "step_pct_of_peak": round(100 * hb / (t["headline_step"] * 1e-6) / 1e9 /
-                                               PEAK_HBM_GBS, 2)}}), flush=True)
+                                               PEAK_HBM_GBS, 2)},
+        "block12": {"bytes": b12, "floor_us": round(t["block12_floor"], 3),
+                    "step_us": round(t["block12_step"], 3),
+                    "step_host_issue_us": round(t["block12_step_host"], 3),
+                    "floor_pct_of_peak": round(100 * b12 / (t["block12_floor"] * 1e-6) / 1e9 /
+                                               PEAK_HBM_GBS, 2),
+                    "step_pct_of_peak": round(100 * b12 / (t["block12_step"] * 1e-6) / 1e9 /
+                                              PEAK_HBM_GBS, 2),
+                    "baseline_md_target_us": 1940.0}}), flush=True)
 
 
 def timed_steps(wl, warmup, steps, hold_cycles):

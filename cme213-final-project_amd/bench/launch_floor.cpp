@@ -17,7 +17,15 @@
 //                 [8192, 768], empty 48, a + b -> c [8192, 3072], empty 96;
 //   headline_step the library's headline step (LayerNorm forward + backward
 //                 on [8192, 768], bias+GELU forward + backward on
-//                 [8192, 3072]).
+//                 [8192, 3072]);
+//   block12_floor BASELINE config 3's bytes in its launch structure, 12 layers
+//                 with their own buffers: per layer two 2-in-2-out adds (the
+//                 residual LayerNorm forwards), a copy (bias+GELU forward),
+//                 then in reverse an a + b -> c with an empty 96-workgroup
+//                 launch (GELU backward + dbias finalize) and two in-place
+//                 c += a + b with empty 48-workgroup launches (the residual
+//                 LayerNorm backwards + finalizes);
+//   block12_step  the library's config-3 step on the same buffers.
 // Each *_floor / *_step case also reports *_host: the host's time to issue
 // one step (the launches only), against which the GPU time shows whether a
 // step is bound by the host's launch rate.
@@ -33,6 +41,7 @@
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <functional>
 #include <string>
 #include <utility>
@@ -75,6 +84,32 @@ __global__ __launch_bounds__(kThreads) void add_kernel(const f4* __restrict__ a,
                                     c + i);
 }
 
+// r = a + b and y = a - b: the residual LayerNorm forward's two reads and two writes.
+__global__ __launch_bounds__(kThreads) void add2_kernel(const f4* __restrict__ a,
+                                                        const f4* __restrict__ b,
+                                                        f4* __restrict__ r, f4* __restrict__ y,
+                                                        long long n) {
+    const long long step = static_cast<long long>(gridDim.x) * kThreads;
+    for (long long i = blockIdx.x * kThreads + threadIdx.x; i < n; i += step) {
+        const f4 x = __builtin_nontemporal_load(a + i);
+        const f4 z = __builtin_nontemporal_load(b + i);
+        __builtin_nontemporal_store(x + z, r + i);
+        __builtin_nontemporal_store(x - z, y + i);
+    }
+}
+
+// c += a + b: the residual LayerNorm backward's three reads and one write.
+__global__ __launch_bounds__(kThreads) void add3_kernel(const f4* __restrict__ a,
+                                                        const f4* __restrict__ b,
+                                                        f4* __restrict__ c, long long n) {
+    const long long step = static_cast<long long>(gridDim.x) * kThreads;
+    for (long long i = blockIdx.x * kThreads + threadIdx.x; i < n; i += step)
+        __builtin_nontemporal_store(__builtin_nontemporal_load(c + i) +
+                                        (__builtin_nontemporal_load(a + i) +
+                                         __builtin_nontemporal_load(b + i)),
+                                    c + i);
+}
+
 hipStream_t st() { return hipStreamPerThread; }
 
 void empty(int blocks) {
@@ -92,11 +127,24 @@ void add(const float* a, const float* b, float* c, long long n) {
                        reinterpret_cast<f4*>(c), n / 4);
 }
 
+void add2(const float* a, const float* b, float* r, float* y, long long n) {
+    hipLaunchKernelGGL(add2_kernel, dim3(kStreamBlocks), dim3(kThreads), 0, st(),
+                       reinterpret_cast<const f4*>(a), reinterpret_cast<const f4*>(b),
+                       reinterpret_cast<f4*>(r), reinterpret_cast<f4*>(y), n / 4);
+}
+
+void add3(const float* a, const float* b, float* c, long long n) {
+    hipLaunchKernelGGL(add3_kernel, dim3(kStreamBlocks), dim3(kThreads), 0, st(),
+                       reinterpret_cast<const f4*>(a), reinterpret_cast<const f4*>(b),
+                       reinterpret_cast<f4*>(c), n / 4);
+}
+
 float* buf(size_t n, float v) {
     float* p = nullptr;
     CK(hipMalloc(&p, n * sizeof(float)));
-    std::vector<float> h(n, v);
-    CK(hipMemcpy(p, h.data(), n * sizeof(float), hipMemcpyHostToDevice));
+    unsigned bits = 0;
+    std::memcpy(&bits, &v, sizeof(bits));
+    CK(hipMemsetD32(reinterpret_cast<hipDeviceptr_t>(p), bits, n));
     return p;
 }
 
@@ -252,6 +300,73 @@ int main(int argc, char** argv) {
         CK(hipFree(db));
         CK(hipFree(dbias));
         CK(hipFree(bias));
+    }
+    // Config 3: GPT-2-small non-GEMM block x12, [8192, 768] / [8192, 3072], each layer
+    // with its own inputs and outputs (as bench.py's block12 workload), one residual-
+    // stream gradient shared by all layers.
+    {
+        const int R = 8192, F = 3072, L = 12;
+        const long long n = 1ll * R * C, nf = 1ll * R * F;
+        struct Layer {
+            float *a, *m, *h, *gy1, *gy2, *gh;                    // inputs
+            float *r1, *r2, *y1, *y2, *m1, *s1, *m2, *s2, *o, *gin;  // outputs
+        };
+        std::vector<Layer> ly(L);
+        for (Layer& e : ly) {
+            e.a = buf(n, 0.5f); e.m = buf(n, 0.25f); e.h = buf(nf, 0.1f);
+            e.gy1 = buf(n, 0.3f); e.gy2 = buf(n, 0.2f); e.gh = buf(nf, 0.4f);
+            e.r1 = buf(n, 0.0f); e.r2 = buf(n, 0.0f); e.y1 = buf(n, 0.0f); e.y2 = buf(n, 0.0f);
+            e.m1 = buf(R, 0.0f); e.s1 = buf(R, 1.0f); e.m2 = buf(R, 0.0f); e.s2 = buf(R, 1.0f);
+            e.o = buf(nf, 0.0f); e.gin = buf(nf, 0.0f);
+        }
+        float* r0 = buf(n, 0.1f);
+        float* gres = buf(n, 0.0f);
+        float* bias = buf(F, 0.01f);
+        float* dg = buf(C, 0.0f);
+        float* db = buf(C, 0.0f);
+        float* dbias = buf(F, 0.0f);
+        CK(hipDeviceSynchronize());
+        rec("block12_floor", [&](int) {
+            const float* r = r0;
+            for (Layer& e : ly) {
+                add2(r, e.a, e.r1, e.y1, n);
+                add2(e.r1, e.m, e.r2, e.y2, n);
+                copy(e.h, e.o, nf);
+                r = e.r2;
+            }
+            for (int l = L - 1; l >= 0; --l) {
+                Layer& e = ly[l];
+                add(e.h, e.gh, e.gin, nf);
+                empty(96);
+                add3(e.gy2, e.r2, gres, n);
+                empty(48);
+                add3(e.gy1, e.r1, gres, n);
+                empty(48);
+            }
+        }, 20 * scale);
+        rec("block12_step", [&](int) {
+            const float* r = r0;
+            for (Layer& e : ly) {
+                residual_layernorm_forward_save(r, e.a, gamma, beta, e.r1, e.y1, e.m1, e.s1, R,
+                                                C);
+                residual_layernorm_forward_save(e.r1, e.m, gamma, beta, e.r2, e.y2, e.m2, e.s2,
+                                                R, C);
+                bias_gelu_forward(e.h, bias, e.o, R, F);
+                r = e.r2;
+            }
+            for (int l = L - 1; l >= 0; --l) {
+                Layer& e = ly[l];
+                gelu_backward_with_bias_backward(e.h, bias, e.gh, e.gin, dbias, R, F);
+                layernorm_backward_residual(e.gy2, e.r2, e.m2, e.s2, gamma, gres, dg, db, R, C);
+                layernorm_backward_residual(e.gy1, e.r1, e.m1, e.s1, gamma, gres, dg, db, R, C);
+            }
+        }, 20 * scale);
+        CK(hipDeviceSynchronize());
+        for (Layer& e : ly)
+            for (float* p : {e.a, e.m, e.h, e.gy1, e.gy2, e.gh, e.r1, e.r2, e.y1, e.y2, e.m1,
+                             e.s1, e.m2, e.s2, e.o, e.gin})
+                CK(hipFree(p));
+        for (float* p : {r0, gres, bias, dg, db, dbias}) CK(hipFree(p));
     }
     CK(hipFree(gamma));
     CK(hipFree(beta));
