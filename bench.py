@@ -316,10 +316,21 @@ def config_suite(hold_us):
     for key, name, warmup, steps, target in CONFIG_SUITE:
         cmd = [sys.executable, os.path.join(ROOT, "bench.py"), "--workload", name, "--steps",
                str(steps), "--warmup", str(warmup), "--no-cpu", "--hold-us", str(hold_us)]
-        r = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
-        if r.returncode != 0:
-            raise SystemExit(f"bench.py: config {name} failed ({r.returncode}):\n{r.stderr[-2000:]}")
-        d = json.loads(r.stdout.strip().splitlines()[-1])
+        # A config that fails is recorded as failed (its command, exit status
+        # and the end of its stderr); the headline line is still printed.
+        try:
+            r = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+            d = json.loads(r.stdout.strip().splitlines()[-1]) if r.returncode == 0 else None
+        except (subprocess.TimeoutExpired, ValueError, IndexError) as e:
+            r, d = None, None
+            err = f"{type(e).__name__}: {e}"
+        if d is None:
+            if r is not None:
+                err = f"exit status {r.returncode}: {r.stderr[-500:]}"
+            print(f"bench.py: config {name} failed ({err})", file=sys.stderr)
+            out[key] = {"workload": WORKLOADS[name], "error": err,
+                        "command": " ".join(["python3", "bench.py"] + cmd[3:])}
+            continue
         us = d["ms_per_step"] * 1e3
         step_bytes = d["config"]["bytes_per_step"]
         gbs = step_bytes / (us * 1e-6) / 1e9

@@ -51,3 +51,30 @@ def test_more_than_one_gpu_is_refused_before_any_gpu_call():
     assert r.returncode == 2, (r.returncode, r.stdout, r.stderr)
     assert r.stdout == ""  # no JSON line
     assert "one GPU" in r.stderr
+
+
+def test_config_block_records_a_failed_config_and_keeps_the_others(monkeypatch):
+    # bench.config_suite runs each config's own bench.py command; a stand-in
+    # for subprocess.run fails one of them and answers the others, so no GPU
+    # is touched: the failure is recorded, the other configs are reported.
+    import json
+    import types
+
+    sys.path.insert(0, ROOT)
+    import bench
+
+    def fake_run(cmd, capture_output, text, timeout):
+        name = cmd[cmd.index("--workload") + 1]
+        if name == "block12":
+            return types.SimpleNamespace(returncode=1, stdout="", stderr="boom")
+        line = {"ms_per_step": 0.02, "config": {"bytes_per_step": 100_000_000}}
+        return types.SimpleNamespace(returncode=0, stdout=json.dumps(line) + "\n", stderr="")
+
+    monkeypatch.setattr(subprocess, "run", fake_run)
+    out = bench.config_suite(400.0)
+    assert set(out) == {k for k, *_ in bench.CONFIG_SUITE}
+    assert "error" in out["config3_block12"] and "boom" in out["config3_block12"]["error"]
+    ok = out["config0_ln"]
+    assert ok["us_per_step"] == 20.0 and ok["gbs"] == 5000.0 and ok["pct_of_peak"] == 62.5
+    assert ok["meets_target"] is False  # 20 us against 11.3 us
+    assert out["config2_embedding"]["meets_target"] is None  # BASELINE.md states no target
