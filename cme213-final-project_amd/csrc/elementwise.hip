@@ -25,6 +25,9 @@
 // over the workgroup's rows in row order and the workgroup writes one
 // partial row; colsum_finalize adds the partial rows in a fixed order.  The
 // reference uses float atomicAdd here (activations.cu:231,271).
+#include <cstring>
+#include <type_traits>
+
 #include "mi_common.hpp"
 
 #ifndef MI_REDUCE_TILES
@@ -98,6 +101,40 @@ __device__ __forceinline__ float gelu_grad(float u) {
 }
 
 // ---------------------------------------------------------------------------
+// Operator arguments.  An Op (at most three pointers) reaches the kernels as
+// three pointer arguments, not as a struct argument.  The library is built
+// with kernel-argument preloading: the first 14 dwords of the argument
+// segment arrive in SGPRs when a wave starts, and the compiler preloads
+// scalar and pointer arguments only, not aggregates.  Passed as a struct, the
+// Op's pointers would cost each kernel a scalar-memory round trip before its
+// first load.  They travel as pointers (not as integers) so that the
+// compiler still knows they address global memory and emits global, not
+// flat, loads and stores.
+// ---------------------------------------------------------------------------
+struct OpWords {
+    const void* w0;
+    const void* w1;
+    const void* w2;
+};
+
+template <class Op>
+OpWords op_words(const Op& op) {
+    static_assert(sizeof(Op) <= sizeof(OpWords), "an Op holds at most three pointers");
+    static_assert(std::is_trivially_copyable<Op>::value, "an Op is a plain pointer struct");
+    const void* w[3] = {nullptr, nullptr, nullptr};
+    std::memcpy(w, &op, sizeof(Op));
+    return {w[0], w[1], w[2]};
+}
+
+template <class Op>
+__device__ __forceinline__ Op op_from(const void* w0, const void* w1, const void* w2) {
+    const void* const w[3] = {w0, w1, w2};
+    Op op;
+    __builtin_memcpy(&op, w, sizeof(Op));
+    return op;
+}
+
+// ---------------------------------------------------------------------------
 // Flat element-wise kernels (no broadcast).  Pointers may alias (the
 // reference allows residual_add(a, b, a)); each element is read and written
 // by one thread, so aliasing is safe without __restrict__.
@@ -144,7 +181,9 @@ struct ReluBwdOp {
 };
 
 template <class Op>
-__global__ __launch_bounds__(kThreads) void flat_kernel(Op op, long long nvec) {
+__global__ __launch_bounds__(kThreads) void flat_kernel(const void* w0, const void* w1,
+                                                        const void* w2, long long nvec) {
+    const Op op = op_from<Op>(w0, w1, w2);
     const long long stride = static_cast<long long>(gridDim.x) * kThreads;
     for (long long i = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x; i < nvec;
          i += stride)
@@ -156,8 +195,9 @@ int launch_flat(const char* name, Op op, long long nvec, hipStream_t st) {
     if (nvec <= 0) return MI_OK;
     long long grid = (nvec + kThreads - 1) / kThreads;
     if (grid > MI_FLAT_MAX_GRID) grid = MI_FLAT_MAX_GRID;
+    const OpWords ow = op_words(op);
     hipLaunchKernelGGL(flat_kernel<Op>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, st,
-                       op, nvec);
+                       ow.w0, ow.w1, ow.w2, nvec);
     return check_launch(name);
 }
 
@@ -183,8 +223,11 @@ int launch_flat(const char* name, Op op, long long nvec, hipStream_t st) {
 // fallback below.
 // ---------------------------------------------------------------------------
 template <int W, int NC, class Op, bool REDUCE>
-__global__ __launch_bounds__(1024) void rowband_kernel(Op op, const float* __restrict__ bias,
+__global__ __launch_bounds__(1024) void rowband_kernel(const void* w0, const void* w1,
+                                                       const void* w2,
+                                                       const float* __restrict__ bias,
                                                        float* __restrict__ part, int rows, int nv) {
+    const Op op = op_from<Op>(w0, w1, w2);
     // Rows per batch (MI_EW_UNROLL, default 1); widths of 3+ vectors per
     // thread use single rows to stay within the 128 VGPRs a 1024-thread
     // workgroup allows (no spills).
@@ -489,9 +532,13 @@ int check_shape(const char* name, int rows, int cols) {
 // vector and walks the rows of slice blockIdx.y in order; one partial row per
 // slice.  Used only for very wide rows, where it is still coalesced.
 template <int W, class Op, bool REDUCE>
-__global__ __launch_bounds__(kThreads) void colslice_kernel(Op op, const float* __restrict__ bias,
+__global__ __launch_bounds__(kThreads) void colslice_kernel(const void* w0,
+                                                            const void* w1,
+                                                            const void* w2,
+                                                            const float* __restrict__ bias,
                                                             float* __restrict__ part, int rows,
                                                             int nv, int rps) {
+    const Op op = op_from<Op>(w0, w1, w2);
     const int j = blockIdx.x * kThreads + threadIdx.x;
     if (j >= nv) return;
     const int r0 = blockIdx.y * rps;
@@ -541,8 +588,14 @@ __device__ __forceinline__ unsigned udiv(unsigned n, const UDiv& u) {
 // Flat grid-stride variant of the non-reducing broadcast kernels: thread i
 // takes vectors i, i + stride, ...; the bias column is i mod nv.
 template <int W, class Op>
-__global__ __launch_bounds__(kThreads) void flatbias_kernel(Op op, const float* __restrict__ bias,
-                                                            unsigned nvec, UDiv row_div) {
+__global__ __launch_bounds__(kThreads) void flatbias_kernel(const void* w0,
+                                                            const void* w1,
+                                                            const void* w2,
+                                                            const float* __restrict__ bias,
+                                                            unsigned nvec, unsigned div_m,
+                                                            int div_l, unsigned div_d) {
+    const Op op = op_from<Op>(w0, w1, w2);
+    const UDiv row_div{div_m, div_l, div_d};
     const unsigned stride = gridDim.x * kThreads;
     for (unsigned i = blockIdx.x * kThreads + threadIdx.x; i < nvec; i += stride) {
         const unsigned j = i - udiv(i, row_div) * row_div.d;
@@ -566,8 +619,12 @@ __global__ __launch_bounds__(kThreads) void flatbias_kernel(Op op, const float* 
 // 3072] bias+GELU and bias+ReLU measured 1.45 us slower than a plain copy of
 // the same bytes with the division and bias load first).
 template <int W, class Op>
-__global__ __launch_bounds__(kThreads) void flatcol_kernel(Op op, const float* __restrict__ bias,
+__global__ __launch_bounds__(kThreads) void flatcol_kernel(const void* w0,
+                                                           const void* w1,
+                                                           const void* w2,
+                                                           const float* __restrict__ bias,
                                                            unsigned nvec, unsigned nv) {
+    const Op op = op_from<Op>(w0, w1, w2);
     const unsigned stride = gridDim.x * kThreads;
     const unsigned base = blockIdx.x * kThreads;
     unsigned i = base + threadIdx.x;
@@ -639,8 +696,9 @@ void launch_band(const BandShape& b, int grid, Op op, const float* bias, float* 
 #define MI_BAND_CASE(NN)                                                                   \
     case NN:                                                                               \
         hipLaunchKernelGGL((rowband_kernel<W, NN, Op, REDUCE>), dim3(grid), dim3(b.threads), \
-                           0, st, op, bias, part, rows, nv);                               \
+                           0, st, ow.w0, ow.w1, ow.w2, bias, part, rows, nv);              \
         break;
+    const OpWords ow = op_words(op);
     switch (b.nc) {
         MI_BAND_CASE(1)
         MI_BAND_CASE(2)
@@ -664,16 +722,18 @@ int launch_rowtile(const char* name, Op op, const float* bias, int rows, int col
     // 2^32 and restart the walk.  Larger tensors take the row bands, whose
     // offsets are 64-bit.
     const long long cgrid = nvec < (1ull << 31) ? flatcol_grid(nvec, nv) : 0;
+    const OpWords ow = op_words(op);
     if (MI_FWD_FLAT && cgrid > 0) {
         hipLaunchKernelGGL((flatcol_kernel<W, Op>), dim3(static_cast<unsigned>(cgrid)),
-                           dim3(kThreads), 0, st, op, bias, static_cast<unsigned>(nvec),
-                           static_cast<unsigned>(nv));
+                           dim3(kThreads), 0, st, ow.w0, ow.w1, ow.w2, bias,
+                           static_cast<unsigned>(nvec), static_cast<unsigned>(nv));
     } else if (MI_FWD_FLAT && nvec < (1ull << 31)) {
         long long grid = (static_cast<long long>(nvec) + kThreads - 1) / kThreads;
         if (grid > MI_FLAT_MAX_GRID) grid = MI_FLAT_MAX_GRID;
+        const UDiv dv = make_udiv(static_cast<unsigned>(nv));
         hipLaunchKernelGGL((flatbias_kernel<W, Op>), dim3(static_cast<unsigned>(grid)),
-                           dim3(kThreads), 0, st, op, bias, static_cast<unsigned>(nvec),
-                           make_udiv(static_cast<unsigned>(nv)));
+                           dim3(kThreads), 0, st, ow.w0, ow.w1, ow.w2, bias,
+                           static_cast<unsigned>(nvec), dv.m, dv.l, dv.d);
     } else if (band_fits(nv)) {
         const BandShape b = band_shape(nv);
         const int grid = rows < kFwdBands ? rows : kFwdBands;
@@ -682,8 +742,8 @@ int launch_rowtile(const char* name, Op op, const float* bias, int rows, int col
         const int rps = static_cast<int>((static_cast<long long>(rows) + kSlices - 1) / kSlices);
         const dim3 grid((nv + kThreads - 1) / kThreads,
                         static_cast<unsigned>((static_cast<long long>(rows) + rps - 1) / rps));
-        hipLaunchKernelGGL((colslice_kernel<W, Op, false>), grid, dim3(kThreads), 0, st, op, bias,
-                           nullptr, rows, nv, rps);
+        hipLaunchKernelGGL((colslice_kernel<W, Op, false>), grid, dim3(kThreads), 0, st, ow.w0,
+                           ow.w1, ow.w2, bias, nullptr, rows, nv, rps);
     }
     return check_launch(name);
 }
@@ -713,8 +773,9 @@ int launch_rowtile_reduce(const char* name, Op op, const float* bias, float* dbi
     } else {
         const int rps = static_cast<int>((static_cast<long long>(rows) + kSlices - 1) / kSlices);
         const dim3 grid((nv + kThreads - 1) / kThreads, P);
-        hipLaunchKernelGGL((colslice_kernel<W, Op, true>), grid, dim3(kThreads), 0, st, op, bias,
-                           part, rows, nv, rps);
+        const OpWords ow = op_words(op);
+        hipLaunchKernelGGL((colslice_kernel<W, Op, true>), grid, dim3(kThreads), 0, st, ow.w0,
+                           ow.w1, ow.w2, bias, part, rows, nv, rps);
     }
     int rc = check_launch(name);
     if (rc != MI_OK) return rc;

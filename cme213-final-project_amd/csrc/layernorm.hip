@@ -64,9 +64,9 @@ constexpr int kBlockThreads = 256;  // generic block-per-row kernels
 // ---------------------------------------------------------------------------
 template <int W, int N, int R, bool SAVE, bool RESID>
 __global__ __launch_bounds__(kFwdWaves * kWave) void ln_fwd_wave_kernel(
-    const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ gamma,
-    const float* __restrict__ beta, float* __restrict__ resid_out, float* __restrict__ out,
-    float* __restrict__ mean_out, float* __restrict__ rstd_out, int rows, int cols, float eps) {
+    int rows, int cols, float eps, const float* __restrict__ a, const float* __restrict__ b,
+    const float* __restrict__ gamma, const float* __restrict__ beta, float* __restrict__ resid_out,
+    float* __restrict__ out, float* __restrict__ mean_out, float* __restrict__ rstd_out) {
     const int lane = threadIdx.x & (kWave - 1);
     const int row0 = (blockIdx.x * kFwdWaves + static_cast<int>(threadIdx.x / kWave)) * R;
     if (!ln_fwd_gb_lds<W, N, R, RESID>() && row0 >= rows) return;  // wave-uniform
@@ -181,9 +181,9 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 // Forward, one block per row, any width (streams the row three times).
 template <bool SAVE, bool RESID>
 __global__ __launch_bounds__(kBlockThreads) void ln_fwd_block_kernel(
-    const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ gamma,
-    const float* __restrict__ beta, float* __restrict__ resid_out, float* __restrict__ out,
-    float* __restrict__ mean_out, float* __restrict__ rstd_out, int rows, int cols, float eps) {
+    int rows, int cols, float eps, const float* __restrict__ a, const float* __restrict__ b,
+    const float* __restrict__ gamma, const float* __restrict__ beta, float* __restrict__ resid_out,
+    float* __restrict__ out, float* __restrict__ mean_out, float* __restrict__ rstd_out) {
     constexpr int NW = kBlockThreads / kWave;
     __shared__ float red[NW];
     const int row = blockIdx.x;
@@ -243,9 +243,9 @@ __host__ __device__ inline bool ln_bwd_flat_combine(int gpb, int cols) {
 
 template <int W, int N, int G, bool ADD, int NWV>
 __global__ __launch_bounds__(NWV * kWave) void ln_bwd_group_kernel(
-    const float* __restrict__ gout, const float* __restrict__ x, const float* __restrict__ mean,
-    const float* __restrict__ rstd, const float* __restrict__ gamma, float* __restrict__ gx,
-    float* __restrict__ part, int rows, int cols) {
+    int rows, int cols, const float* __restrict__ gout, const float* __restrict__ x,
+    const float* __restrict__ mean, const float* __restrict__ rstd, const float* __restrict__ gamma,
+    float* __restrict__ gx, float* __restrict__ part) {
     constexpr int GPB = NWV / G;  // row groups per workgroup
     constexpr int GT = G * kWave;       // threads per group
     extern __shared__ float lds[];
@@ -482,9 +482,9 @@ __global__ __launch_bounds__(NWV * kWave) void ln_bwd_group_kernel(
 // block's partial row (only this block touches it, so plain loads/stores).
 template <bool ADD>
 __global__ __launch_bounds__(kBlockThreads) void ln_bwd_block_kernel(
-    const float* __restrict__ gout, const float* __restrict__ x, const float* __restrict__ mean,
-    const float* __restrict__ rstd, const float* __restrict__ gamma, float* __restrict__ gx,
-    float* __restrict__ part, int rows, int cols) {
+    int rows, int cols, const float* __restrict__ gout, const float* __restrict__ x,
+    const float* __restrict__ mean, const float* __restrict__ rstd, const float* __restrict__ gamma,
+    float* __restrict__ gx, float* __restrict__ part) {
     constexpr int NW = kBlockThreads / kWave;
     __shared__ float red[NW];
     float* pg = part + static_cast<size_t>(blockIdx.x) * 2 * cols;
@@ -559,8 +559,8 @@ void launch_fwd_wave(int n, hipStream_t st, const float* a, const float* b, cons
 #define MI_LN_FWD_CASE(NN)                                                                     \
     case NN:                                                                                   \
         hipLaunchKernelGGL((ln_fwd_wave_kernel<W, NN, R, SAVE, RESID>), grid, block,              \
-                           (ln_fwd_gb_lds<W, NN, R, RESID>() ? 2 * cols * sizeof(float) : 0), st, a, \
-                           b, gamma, beta, ro, out, mo, so, rows, cols, eps);                  \
+                           (ln_fwd_gb_lds<W, NN, R, RESID>() ? 2 * cols * sizeof(float) : 0), st,    \
+                           rows, cols, eps, a, b, gamma, beta, ro, out, mo, so);               \
         break;
     switch (n) {
         MI_LN_FWD_CASE(1)
@@ -608,7 +608,7 @@ int ln_forward_impl(const char* name, const float* a, const float* b, const floa
                                                cols, eps);
     } else {
         hipLaunchKernelGGL((ln_fwd_block_kernel<SAVE, RESID>), dim3(rows), dim3(kBlockThreads), 0,
-                           st, a, b, gamma, beta, ro, out, mo, so, rows, cols, eps);
+                           st, rows, cols, eps, a, b, gamma, beta, ro, out, mo, so);
     }
     return check_launch(name);
 }
@@ -677,22 +677,22 @@ void launch_bwd_group(const BwdPlan& p, hipStream_t st, const float* g, const fl
     if constexpr (ADD && ((G == 1 && N <= 3) || (G == 4 && N <= 2))) {
         if (p.waves == 16) {
             hipLaunchKernelGGL((ln_bwd_group_kernel<W, N, G, ADD, 16>), dim3(p.blocks),
-                               dim3(16 * kWave), p.lds, st, g, x, m, s, gamma, gx, part, rows,
-                               cols);
+                               dim3(16 * kWave), p.lds, st, rows, cols, g, x, m, s, gamma, gx,
+                               part);
             return;
         }
     }
     if constexpr (G == 4 && N == 4) {
         if (p.waves == 4) {
             hipLaunchKernelGGL((ln_bwd_group_kernel<W, N, G, ADD, 4>), dim3(p.blocks),
-                               dim3(4 * kWave), p.lds, st, g, x, m, s, gamma, gx, part, rows,
-                               cols);
+                               dim3(4 * kWave), p.lds, st, rows, cols, g, x, m, s, gamma, gx,
+                               part);
             return;
         }
     }
     hipLaunchKernelGGL((ln_bwd_group_kernel<W, N, G, ADD, kBwdWaves>), dim3(p.blocks),
-                       dim3(kBwdWaves * kWave), p.lds, st, g, x, m, s, gamma, gx, part, rows,
-                       cols);
+                       dim3(kBwdWaves * kWave), p.lds, st, rows, cols, g, x, m, s, gamma, gx,
+                       part);
 }
 
 template <int W, int G, bool ADD>
@@ -760,7 +760,7 @@ int ln_backward_launch(const char* name, const BwdPlan& p, const float* g, const
             dispatch_bwd_g<1, ADD>(p, st, g, x, m, s, gamma, gx, part, rows, cols);
     } else {
         hipLaunchKernelGGL((ln_bwd_block_kernel<ADD>), dim3(p.blocks), dim3(kBlockThreads), 0, st,
-                           g, x, m, s, gamma, gx, part, rows, cols);
+                           rows, cols, g, x, m, s, gamma, gx, part);
     }
     int rc = check_launch(name);
     if (rc != MI_OK) return rc;
