@@ -226,14 +226,16 @@ template <int W, int NC, class Op, bool REDUCE>
 __global__ __launch_bounds__(1024) void rowband_kernel(const void* w0, const void* w1,
                                                        const void* w2,
                                                        const float* __restrict__ bias,
-                                                       float* __restrict__ part, int rows, int nv) {
+                                                       float* __restrict__ part, int rows, int nv,
+                                                       int T, int G) {
     const Op op = op_from<Op>(w0, w1, w2);
     // Rows per batch (MI_EW_UNROLL, default 1); widths of 3+ vectors per
     // thread use single rows to stay within the 128 VGPRs a 1024-thread
     // workgroup allows (no spills).
     constexpr int U = NC <= 2 ? kUnroll : 1;
-    const int T = blockDim.x;
-    const int G = gridDim.x;
+    // T and G (blockDim.x and gridDim.x) arrive as arguments, preloaded with
+    // the others: read through the dispatch they are scalar loads in front
+    // of the first row's loads.
     fvec<W> bv[NC], acc[NC];
 #pragma unroll
     for (int k = 0; k < NC; ++k) {
@@ -696,7 +698,8 @@ void launch_band(const BandShape& b, int grid, Op op, const float* bias, float* 
 #define MI_BAND_CASE(NN)                                                                   \
     case NN:                                                                               \
         hipLaunchKernelGGL((rowband_kernel<W, NN, Op, REDUCE>), dim3(grid), dim3(b.threads), \
-                           0, st, ow.w0, ow.w1, ow.w2, bias, part, rows, nv);              \
+                           0, st, ow.w0, ow.w1, ow.w2, bias, part, rows, nv, b.threads,    \
+                           grid);                                                          \
         break;
     const OpWords ow = op_words(op);
     switch (b.nc) {

@@ -181,9 +181,9 @@ constexpr int kPosChunk = 5; // batch rows per group of loads afterwards
 // 128 VGPRs at most, so that two 8-wave workgroups fit on a CU.
 template <int W, int NCH, bool POS>
 __global__ __launch_bounds__(kOwnThreads) __attribute__((amdgpu_waves_per_eu(4))) void
-emb_bwd_owner_kernel(const int* __restrict__ ids, int n, int vocab, bool vec_ids,
-                     const float* __restrict__ g, float* __restrict__ table, int dim,
-                     float* __restrict__ gpos, int batch, int seq) {
+emb_bwd_owner_kernel(int n, int vocab, int dim, int batch, int seq, int vec_ids, int nblk,
+                     const int* __restrict__ ids, const float* __restrict__ g,
+                     float* __restrict__ table, float* __restrict__ gpos) {
     __shared__ __align__(16) int s_id[kOwnCap];  // list in position order
     __shared__ int s_pos[kOwnCap];
     __shared__ int s_sid[kOwnCap];  // list sorted by id
@@ -195,8 +195,9 @@ emb_bwd_owner_kernel(const int* __restrict__ ids, int n, int vocab, bool vec_ids
     // Uniform over the wave; readfirstlane lets the compiler see that, so
     // branches on it are scalar branches, not exec-masked ones.
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
-    // gridDim.x is a power of two, so id % gridDim.x is a mask.
-    const unsigned kmask = gridDim.x - 1u;
+    // nblk (= gridDim.x, passed and preloaded with the other arguments) is a
+    // power of two, so id % nblk is a mask.
+    const unsigned kmask = static_cast<unsigned>(nblk) - 1u;
     const unsigned k = blockIdx.x;
     const int nv = dim / W;
 
@@ -348,7 +349,7 @@ emb_bwd_owner_kernel(const int* __restrict__ ids, int n, int vocab, bool vec_ids
 
     // Position gradient, first round: requests issued now, summed below.
     const long long pvec = POS ? static_cast<long long>(seq) * nv : 0;   // position vectors
-    const long long pstride = static_cast<long long>(gridDim.x) * kOwnThreads;
+    const long long pstride = static_cast<long long>(nblk) * kOwnThreads;
     // A thread's first position vector, below kOwnMaxK * kOwnThreads = 2^18:
     // 32 bits.  Held as a 64-bit value it was spilled to scratch, and its
     // reload waited for every outstanding load.
@@ -606,8 +607,9 @@ void launch_owner(const float* grad_out, const int* tokens, float* grad_table, f
     // 4 (wider rows loop over column chunks).
     const int nch = nv <= kWave ? 1 : nv <= 2 * kWave ? 2 : nv <= 3 * kWave ? 3 : 4;
 #define MI_OWNER_CASE(WW, NN)                                                                  \
-    hipLaunchKernelGGL((emb_bwd_owner_kernel<WW, NN, POS>), grid, block, 0, st, tokens,       \
-                       batch_seq, vocab, vec_ids, grad_out, grad_table, dim, grad_pos, batch, seq)
+    hipLaunchKernelGGL((emb_bwd_owner_kernel<WW, NN, POS>), grid, block, 0, st, batch_seq,    \
+                       vocab, dim, batch, seq, vec_ids ? 1 : 0, 1 << log2k, tokens, grad_out, \
+                       grad_table, grad_pos)
     switch ((v4 ? 10 : 0) + nch) {
         case 11: MI_OWNER_CASE(4, 1); break;
         case 12: MI_OWNER_CASE(4, 2); break;

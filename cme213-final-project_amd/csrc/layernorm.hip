@@ -243,9 +243,14 @@ __host__ __device__ inline bool ln_bwd_flat_combine(int gpb, int cols) {
 
 template <int W, int N, int G, bool ADD, int NWV>
 __global__ __launch_bounds__(NWV * kWave) void ln_bwd_group_kernel(
-    int rows, int cols, const float* __restrict__ gout, const float* __restrict__ x,
-    const float* __restrict__ mean, const float* __restrict__ rstd, const float* __restrict__ gamma,
-    float* __restrict__ gx, float* __restrict__ part) {
+    int rows, int cols, int nblk, const float* __restrict__ gout, const float* __restrict__ x,
+    const float* __restrict__ gamma, float* __restrict__ gx, const float* __restrict__ mean,
+    const float* __restrict__ rstd, float* __restrict__ part) {
+    // Argument order: the first 14 dwords (rows .. mean) are preloaded into
+    // SGPRs.  They hold everything the first row's loads and the loop's
+    // hoisted addresses need (gx's base address is set up before the loop);
+    // rstd is first read after the row's data loads are issued, and part at
+    // the end, so their scalar loads are off the critical path.
     constexpr int GPB = NWV / G;  // row groups per workgroup
     constexpr int GT = G * kWave;       // threads per group
     extern __shared__ float lds[];
@@ -267,7 +272,9 @@ __global__ __launch_bounds__(NWV * kWave) void ln_bwd_group_kernel(
         ab[k] = vzero<W>();
     }
 
-    const int stride = gridDim.x * GPB;
+    // nblk = gridDim.x, passed (and preloaded) with the other arguments: read
+    // through the dispatch it is a scalar load in front of the first row.
+    const int stride = nblk * GPB;
     // One row's inputs.  Every load is unconditional (row and column indices
     // are clamped into the tensor, masked slots are zeroed after the load),
     // so the loads carry no branches.
@@ -482,9 +489,9 @@ __global__ __launch_bounds__(NWV * kWave) void ln_bwd_group_kernel(
 // block's partial row (only this block touches it, so plain loads/stores).
 template <bool ADD>
 __global__ __launch_bounds__(kBlockThreads) void ln_bwd_block_kernel(
-    int rows, int cols, const float* __restrict__ gout, const float* __restrict__ x,
-    const float* __restrict__ mean, const float* __restrict__ rstd, const float* __restrict__ gamma,
-    float* __restrict__ gx, float* __restrict__ part) {
+    int rows, int cols, float* __restrict__ part, const float* __restrict__ gout,
+    const float* __restrict__ x, const float* __restrict__ mean, const float* __restrict__ rstd,
+    const float* __restrict__ gamma, float* __restrict__ gx) {
     constexpr int NW = kBlockThreads / kWave;
     __shared__ float red[NW];
     float* pg = part + static_cast<size_t>(blockIdx.x) * 2 * cols;
@@ -677,22 +684,22 @@ void launch_bwd_group(const BwdPlan& p, hipStream_t st, const float* g, const fl
     if constexpr (ADD && ((G == 1 && N <= 3) || (G == 4 && N <= 2))) {
         if (p.waves == 16) {
             hipLaunchKernelGGL((ln_bwd_group_kernel<W, N, G, ADD, 16>), dim3(p.blocks),
-                               dim3(16 * kWave), p.lds, st, rows, cols, g, x, m, s, gamma, gx,
-                               part);
+                               dim3(16 * kWave), p.lds, st, rows, cols, p.blocks, g, x, gamma,
+                               gx, m, s, part);
             return;
         }
     }
     if constexpr (G == 4 && N == 4) {
         if (p.waves == 4) {
             hipLaunchKernelGGL((ln_bwd_group_kernel<W, N, G, ADD, 4>), dim3(p.blocks),
-                               dim3(4 * kWave), p.lds, st, rows, cols, g, x, m, s, gamma, gx,
-                               part);
+                               dim3(4 * kWave), p.lds, st, rows, cols, p.blocks, g, x, gamma,
+                               gx, m, s, part);
             return;
         }
     }
     hipLaunchKernelGGL((ln_bwd_group_kernel<W, N, G, ADD, kBwdWaves>), dim3(p.blocks),
-                       dim3(kBwdWaves * kWave), p.lds, st, rows, cols, g, x, m, s, gamma, gx,
-                       part);
+                       dim3(kBwdWaves * kWave), p.lds, st, rows, cols, p.blocks, g, x, gamma,
+                       gx, m, s, part);
 }
 
 template <int W, int G, bool ADD>
@@ -760,7 +767,7 @@ int ln_backward_launch(const char* name, const BwdPlan& p, const float* g, const
             dispatch_bwd_g<1, ADD>(p, st, g, x, m, s, gamma, gx, part, rows, cols);
     } else {
         hipLaunchKernelGGL((ln_bwd_block_kernel<ADD>), dim3(p.blocks), dim3(kBlockThreads), 0, st,
-                           rows, cols, g, x, m, s, gamma, gx, part);
+                           rows, cols, part, g, x, m, s, gamma, gx);
     }
     int rc = check_launch(name);
     if (rc != MI_OK) return rc;
