@@ -309,6 +309,21 @@ __global__ __launch_bounds__(NWV * kWave) void ln_bwd_group_kernel(
 #pragma unroll
             for (int e = 0; e < W; ++e) go[k].v[e] = ok ? cur.go[k].v[e] : 0.0f;
         }
+        // The accumulated gradient's vectors (ADD), requested together once
+        // the row's inputs have arrived (clamped, unconditional), so that the
+        // row's stores wait for one round trip.  Loaded one by one in the
+        // store loop, each load also waited for the previous vector's store
+        // (the vector-memory counter retires in order): block x48 8339-8348
+        // -> 8247-8257 us, block x12 unchanged (1936 us), same box, three
+        // A/B rounds.
+        [[maybe_unused]] fvec<W> acc_in[N];
+        if constexpr (ADD) {
+#pragma unroll
+            for (int k = 0; k < N; ++k) {
+                const int j = t + k * GT;
+                acc_in[k] = sload<W>(gx + off, j < nv ? j : nv - 1);
+            }
+        }
         float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
         for (int k = 0; k < N; ++k)
@@ -352,12 +367,16 @@ __global__ __launch_bounds__(NWV * kWave) void ln_bwd_group_kernel(
             }
         }
         if (valid) {
+            if constexpr (ADD) {
+#pragma unroll
+                for (int k = 0; k < N; ++k) consume(acc_in[k]);
+            }
 #pragma unroll
             for (int k = 0; k < N; ++k) {
                 const int j = t + k * GT;
                 if (j < nv) {
                     fvec<W> d;
-                    if constexpr (ADD) d = sload<W>(gx + off, j);
+                    if constexpr (ADD) d = acc_in[k];
 #pragma unroll
                     for (int e = 0; e < W; ++e) {
                         const float xh = (cur.xv[k].v[e] - mu) * is;
