@@ -7,7 +7,8 @@ The boundaries crossed: rows-per-wave choice of the LN forward (6144 rows,
 backward row (2048 and 8192 columns), the register-resident widths against
 the block-per-row fallbacks, vector (W = 4) against scalar columns (width not
 a multiple of 4, or a tensor that starts 4 bytes into its allocation), the
-flat against the row-band form of the bias operators, and the embedding
+flat against the row-band form of the bias operators (one to four column
+vectors per row-band thread), and the embedding
 backward's owner count (a power of two from about 32 tokens each)."""
 import numpy as np
 import pytest
@@ -80,8 +81,12 @@ def test_layernorm_shape_sweep(dev, rows, cols, offset):
     assert_colsum("dbeta", host(DB), db_o, g)
 
 
+# The fixed cases include rows of 3 and 4 column vectors per row-band thread
+# (12288 and 16000 columns) with more rows than row bands, where the kernel's
+# workgroup and grid sizes (passed as arguments) set every thread's columns
+# and rows.
 GELU_SHAPES = _shapes(202, 10, 4 << 20, [(8192, 3, 0), (1, 16384, 0), (513, 4097, 1),
-                                         (4096, 6400, 0)])
+                                         (4096, 6400, 0), (350, 12288, 0), (300, 16000, 0)])
 
 
 @pytest.mark.parametrize("rows,cols,offset", GELU_SHAPES)
